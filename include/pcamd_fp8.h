@@ -1,0 +1,134 @@
+/*
+ * pcamd_fp8.h - C ABI of the MI355X (gfx950) FP8 hot path.
+ *
+ * One shared library, libpcamd_fp8.so, exports these functions. They take raw
+ * device pointers, element strides (in elements, not bytes) and sizes, launch
+ * asynchronously on the given hipStream_t (passed as void*), never allocate
+ * device memory, keep no mutable global state and are reentrant. Every
+ * function returns PCAMD_OK (0) or a negative status; pcamd_last_error()
+ * returns a thread-local description of the most recent failure.
+ *
+ * Reference interfaces replaced (paths relative to xuOAO/practice_cuda):
+ *   pcamd_quant_block   <- fp8_training/fp8_bench/impls/triton_per_block.py:60-150
+ *                          (launches kernels/quant/per_block.py:6-48)
+ *   pcamd_quant_channel <- fp8_training/fp8_bench/impls/triton_per_channel.py:90-219
+ *                          (launches kernels/quant/per_channel.py:35-102, :105-267)
+ *   pcamd_quant_tensor  <- fp8_training/fp8_bench/impls/triton_per_tensor.py:28-95
+ *                          and kernels/fp8_bmm/fp8_warper.py:9-77
+ *   pcamd_bmm_scaled    <- impls/triton_per_block.py:232-420 (block scales),
+ *                          impls/triton_per_channel.py:271-427 (channel scales),
+ *                          impls/triton_per_tensor.py:140-306 and
+ *                          kernels/fp8_bmm/fp8_warper.py:79-129 (tensor scale)
+ */
+#ifndef PCAMD_FP8_H
+#define PCAMD_FP8_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define PCAMD_ABI_VERSION 1
+
+/* status codes */
+#define PCAMD_OK 0
+#define PCAMD_ERR_INVALID (-1)     /* bad argument (shape, stride, pointer, code) */
+#define PCAMD_ERR_UNSUPPORTED (-2) /* valid but not implemented combination */
+#define PCAMD_ERR_LAUNCH (-3)      /* hipGetLastError() after launch */
+
+/* element type codes */
+#define PCAMD_F32 0
+#define PCAMD_BF16 1
+#define PCAMD_F16 2
+#define PCAMD_E4M3FN 3 /* OCP fp8 e4m3fn: max 448, no inf, NaN = 0x7f/0xff */
+#define PCAMD_E5M2 4   /* OCP fp8 e5m2: max 57344, inf = 0x7c */
+
+/* BMM scale modes */
+#define PCAMD_SCALE_BLOCK 0   /* sa[b, m/qbm, k/qbk], sb[b, k/qbk, n/qbn] */
+#define PCAMD_SCALE_CHANNEL 1 /* sa[b, m], sb[b, n] */
+#define PCAMD_SCALE_TENSOR 2  /* sa[0] (and sb[0] when scales_are_quant) */
+
+/* BMM epilogue activations */
+#define PCAMD_ACT_NONE 0
+#define PCAMD_ACT_GELU 1 /* exact: 0.5 x (1 + erf(x / sqrt 2)) */
+
+int pcamd_abi_version(void);
+const char *pcamd_last_error(void);
+
+/*
+ * Per-block quantization of x[batch, m, n] into fp8 y with one fp32 dequant
+ * scale per block_m x block_n tile (block sizes are powers of two).
+ * Per block: amax = max|x|; s = max(amax, eps); qs = fp8_max / s;
+ * scale[b, i, j] = 1 / qs; y = fp8_rne(clamp(x * qs, -fp8_max, fp8_max)).
+ * Replaces fp8_training/fp8_bench/impls/triton_per_block.py:60-150.
+ */
+int pcamd_quant_block(const void *x, int x_dtype, int64_t batch, int64_t m,
+                      int64_t n, int64_t sxb, int64_t sxm, int64_t sxn,
+                      void *y, int y_dtype, int64_t syb, int64_t sym,
+                      int64_t syn, float *scale, int64_t ssb, int64_t ssm,
+                      int64_t ssn, int64_t block_m, int64_t block_n,
+                      float fp8_max, float eps, void *stream);
+
+/*
+ * Per-channel quantization. channel_axis = -2: one scale per row (reduce over
+ * n); channel_axis = -1: one scale per column (reduce over m).
+ * s = max(amax, eps); qs = fp8_max / s; scale[b, c] = s / fp8_max;
+ * y = fp8_rne(clamp(x * qs, -fp8_max, fp8_max)).
+ * Replaces fp8_training/fp8_bench/impls/triton_per_channel.py:90-219.
+ */
+int pcamd_quant_channel(const void *x, int x_dtype, int64_t batch, int64_t m,
+                        int64_t n, int64_t sxb, int64_t sxm, int64_t sxn,
+                        void *y, int y_dtype, int64_t syb, int64_t sym,
+                        int64_t syn, float *scale, int64_t ssb, int64_t ssc,
+                        int channel_axis, float fp8_max, float eps,
+                        void *stream);
+
+/*
+ * Per-tensor quantization: amax over the whole tensor, s = max(amax, eps),
+ * qs = fp8_max / s, scale[0] = 1 / qs, y = fp8_rne(clamp(x * qs)).
+ * quant_scale_out (may be NULL) receives qs. Both scalars are device fp32.
+ * Replaces impls/triton_per_tensor.py:28-95 and fp8_bmm/fp8_warper.py:9-77.
+ */
+int pcamd_quant_tensor(const void *x, int x_dtype, int64_t batch, int64_t m,
+                       int64_t n, int64_t sxb, int64_t sxm, int64_t sxn,
+                       void *y, int y_dtype, int64_t syb, int64_t sym,
+                       int64_t syn, float *scale, float *quant_scale_out,
+                       float fp8_max, float eps, void *stream);
+
+/*
+ * Scaled FP8 batched GEMM: c[b, m, n] = act(sum_k a[b, m, k] b[b, k, n] *
+ * scale + bias[b, m, n]) with fp32 accumulation, a/b fp8 of the same code.
+ * Block mode applies sa[b, m/qbm, kq] * sb[b, kq, n/qbn] to each qbk-wide
+ * partial sum (qbk a multiple of 128); channel mode multiplies the full sum by
+ * sa[b, m] * sb[b, n]; tensor mode by sa[0]. scales_are_quant = 1 means the
+ * scales are quant scales and the product is inverted (1 / (sa * sb)).
+ * bias may be NULL. Strides are in elements; a must be contiguous along k or
+ * m, b along n or k, c and bias along n.
+ */
+int pcamd_bmm_scaled(const void *a, const void *b, int ab_dtype,
+                     int64_t batch, int64_t m, int64_t n, int64_t k,
+                     int64_t sab, int64_t sam, int64_t sak, int64_t sbb,
+                     int64_t sbk, int64_t sbn, void *c, int c_dtype,
+                     int64_t scb, int64_t scm, int64_t scn, const void *bias,
+                     int bias_dtype, int64_t sbiasb, int64_t sbiasm,
+                     int64_t sbiasn, const float *sa, int64_t ssab,
+                     int64_t ssa1, int64_t ssa2, const float *sb,
+                     int64_t ssbb, int64_t ssb1, int64_t ssb2, int scale_mode,
+                     int scales_are_quant, int64_t qbm, int64_t qbk,
+                     int64_t qbn, int activation, void *stream);
+
+/*
+ * Device self-test of the fp32 -> fp8 conversion used by the quantizers:
+ * compares the gfx950 hardware conversion with an integer restatement of
+ * round-to-nearest-even over every fp32 bit pattern with |x| <= fp8 max.
+ * result (device, 4 x uint32) receives {mismatches, first mismatching
+ * pattern, checked count low 32 bits, 0}. fmt is PCAMD_E4M3FN or PCAMD_E5M2.
+ */
+int pcamd_selftest_fp8_convert(int fmt, uint32_t *result, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* PCAMD_FP8_H */

@@ -1,0 +1,227 @@
+// fp8_common.h - device helpers shared by the gfx950 FP8 kernels.
+//
+// Element conversions, 8-element "chunk" loads (one 128-bit load for 16-bit
+// inputs, two for fp32), wavefront max reductions over aligned lane groups
+// (DPP inside a 16-lane row, ds_swizzle/bpermute beyond), and fp32 -> OCP
+// fp8 packing through the gfx950 hardware converters.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/pcamd_fp8.h"
+
+#define PCAMD_DEV __device__ __forceinline__
+
+namespace pcamd {
+
+constexpr int kF32 = PCAMD_F32;
+constexpr int kBF16 = PCAMD_BF16;
+constexpr int kF16 = PCAMD_F16;
+constexpr int kE4M3 = PCAMD_E4M3FN;
+constexpr int kE5M2 = PCAMD_E5M2;
+
+// ---------------------------------------------------------------------------
+// element conversions
+// ---------------------------------------------------------------------------
+PCAMD_DEV float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
+PCAMD_DEV float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xFFFF0000u); }
+PCAMD_DEV float f16_lo(uint32_t w) {
+  return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(w & 0xFFFFu)));
+}
+PCAMD_DEV float f16_hi(uint32_t w) {
+  return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(w >> 16)));
+}
+
+template <int DT>
+PCAMD_DEV float load_one(const void* base, int64_t off) {
+  if constexpr (DT == kF32) {
+    return static_cast<const float*>(base)[off];
+  } else if constexpr (DT == kBF16) {
+    return __uint_as_float(static_cast<uint32_t>(static_cast<const uint16_t*>(base)[off]) << 16);
+  } else {
+    return static_cast<float>(static_cast<const _Float16*>(base)[off]);
+  }
+}
+
+template <int DT>
+constexpr int elem_bytes() {
+  return DT == kF32 ? 4 : 2;
+}
+
+// Eight consecutive input elements as raw bits.
+template <int DT>
+struct Chunk {
+  uint4 r[DT == kF32 ? 2 : 1];
+};
+
+template <int DT>
+PCAMD_DEV void load_chunk(Chunk<DT>& c, const void* p) {
+  const uint4* q = static_cast<const uint4*>(p);
+  c.r[0] = q[0];
+  if constexpr (DT == kF32) c.r[1] = q[1];
+}
+
+template <int DT>
+PCAMD_DEV void zero_chunk(Chunk<DT>& c) {
+  c.r[0] = make_uint4(0, 0, 0, 0);
+  if constexpr (DT == kF32) c.r[1] = make_uint4(0, 0, 0, 0);
+}
+
+template <int DT>
+PCAMD_DEV void unpack_chunk(const Chunk<DT>& c, float (&v)[8]) {
+  if constexpr (DT == kF32) {
+    v[0] = __uint_as_float(c.r[0].x); v[1] = __uint_as_float(c.r[0].y);
+    v[2] = __uint_as_float(c.r[0].z); v[3] = __uint_as_float(c.r[0].w);
+    v[4] = __uint_as_float(c.r[1].x); v[5] = __uint_as_float(c.r[1].y);
+    v[6] = __uint_as_float(c.r[1].z); v[7] = __uint_as_float(c.r[1].w);
+  } else if constexpr (DT == kBF16) {
+    v[0] = bf16_lo(c.r[0].x); v[1] = bf16_hi(c.r[0].x);
+    v[2] = bf16_lo(c.r[0].y); v[3] = bf16_hi(c.r[0].y);
+    v[4] = bf16_lo(c.r[0].z); v[5] = bf16_hi(c.r[0].z);
+    v[6] = bf16_lo(c.r[0].w); v[7] = bf16_hi(c.r[0].w);
+  } else {
+    v[0] = f16_lo(c.r[0].x); v[1] = f16_hi(c.r[0].x);
+    v[2] = f16_lo(c.r[0].y); v[3] = f16_hi(c.r[0].y);
+    v[4] = f16_lo(c.r[0].z); v[5] = f16_hi(c.r[0].z);
+    v[6] = f16_lo(c.r[0].w); v[7] = f16_hi(c.r[0].w);
+  }
+}
+
+// max |x| over the 8 elements of a chunk
+template <int DT>
+PCAMD_DEV float chunk_amax(const Chunk<DT>& c) {
+  float v[8];
+  unpack_chunk<DT>(c, v);
+  float a = fmaxf(fabsf(v[0]), fabsf(v[1]));
+  float b = fmaxf(fabsf(v[2]), fabsf(v[3]));
+  float d = fmaxf(fabsf(v[4]), fabsf(v[5]));
+  float e = fmaxf(fabsf(v[6]), fabsf(v[7]));
+  return fmaxf(fmaxf(a, b), fmaxf(d, e));
+}
+
+// ---------------------------------------------------------------------------
+// wavefront reductions: max over aligned groups of LANES lanes (power of 2)
+// ---------------------------------------------------------------------------
+template <int CTRL>
+PCAMD_DEV float dpp_mov(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+
+constexpr int kDppQuadXor1 = 0xB1;     // quad_perm [1,0,3,2]
+constexpr int kDppQuadXor2 = 0x4E;     // quad_perm [2,3,0,1]
+constexpr int kDppRowHalfMirror = 0x141;
+constexpr int kDppRowMirror = 0x140;
+
+// All 64 lanes must be active when this is called.
+template <int LANES>
+PCAMD_DEV float group_max(float v) {
+  if constexpr (LANES >= 2) v = fmaxf(v, dpp_mov<kDppQuadXor1>(v));
+  if constexpr (LANES >= 4) v = fmaxf(v, dpp_mov<kDppQuadXor2>(v));
+  // after the quad steps every lane holds its quad's max; mirroring inside 8
+  // (then 16) lanes pairs each quad with the other quad of the half-row (row)
+  if constexpr (LANES >= 8) v = fmaxf(v, dpp_mov<kDppRowHalfMirror>(v));
+  if constexpr (LANES >= 16) v = fmaxf(v, dpp_mov<kDppRowMirror>(v));
+  if constexpr (LANES >= 32) {
+    // swap the two 16-lane rows of each 32-lane half (bit-mode swizzle, xor 16)
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x401F)));
+  }
+  if constexpr (LANES >= 64) v = fmaxf(v, __shfl_xor(v, 32, 64));
+  return v;
+}
+
+// ---------------------------------------------------------------------------
+// fp32 -> fp8 (OCP e4m3fn / e5m2), round to nearest even
+// ---------------------------------------------------------------------------
+// Integer restatement (same algorithm as the CPU oracle); used by the
+// conversion self-test and available as a fallback path.
+template <int FMT>
+PCAMD_DEV uint32_t sw_encode(float f) {
+  uint32_t u = __float_as_uint(f);
+  uint32_t sign = (u >> 24) & 0x80u;
+  uint32_t a = u & 0x7FFFFFFFu;
+  if constexpr (FMT == kE4M3) {
+    if (a > 0x7F800000u || a >= 0x43F00000u) return sign | 0x7Fu;
+    if (a < 0x3C800000u) return sign | static_cast<uint32_t>(__builtin_rintf(__uint_as_float(a) * 512.0f));
+    uint32_t r = a + 0x7FFFFu + ((a >> 20) & 1u);
+    return sign | ((r >> 20) - ((127u - 7u) << 3));
+  } else {
+    if (a > 0x7F800000u) return sign | 0x7Fu;
+    if (a >= 0x47800000u) return sign | 0x7Cu;
+    if (a < 0x38800000u) return sign | static_cast<uint32_t>(__builtin_rintf(__uint_as_float(a) * 65536.0f));
+    uint32_t r = a + 0xFFFFFu + ((a >> 21) & 1u);
+    return sign | ((r >> 21) - ((127u - 15u) << 2));
+  }
+}
+
+// gfx950 v_cvt_pk_{fp8,bf8}_f32: two fp32 -> two OCP fp8 in the selected
+// 16-bit half of the destination (src0 -> low byte).
+template <int FMT>
+PCAMD_DEV uint32_t hw_pack4(float a, float b, float c, float d) {
+  if constexpr (FMT == kE4M3) {
+    int w = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
+    return static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_fp8_f32(c, d, w, true));
+  } else {
+    int w = __builtin_amdgcn_cvt_pk_bf8_f32(a, b, 0, false);
+    return static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_bf8_f32(c, d, w, true));
+  }
+}
+
+template <int FMT>
+PCAMD_DEV uint32_t pack4(float a, float b, float c, float d) {
+#ifdef PCAMD_SOFTWARE_FP8_CONVERT
+  return sw_encode<FMT>(a) | (sw_encode<FMT>(b) << 8) | (sw_encode<FMT>(c) << 16) |
+         (sw_encode<FMT>(d) << 24);
+#else
+  return hw_pack4<FMT>(a, b, c, d);
+#endif
+}
+
+// tl.clamp(v, -max, max)
+PCAMD_DEV float clamp_sym(float v, float hi) { return __builtin_amdgcn_fmed3f(v, -hi, hi); }
+
+// quantize a chunk: 8 elements -> 8 fp8 bytes (little-endian in a uint2)
+template <int DT, int FMT>
+PCAMD_DEV uint2 quant_chunk(const Chunk<DT>& c, float qs, float fp8_max) {
+  float v[8];
+  unpack_chunk<DT>(c, v);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) v[i] = clamp_sym(v[i] * qs, fp8_max);
+  return make_uint2(pack4<FMT>(v[0], v[1], v[2], v[3]), pack4<FMT>(v[4], v[5], v[6], v[7]));
+}
+
+template <int DT, int FMT>
+PCAMD_DEV uint32_t quant_one(float v, float qs, float fp8_max) {
+  float q = clamp_sym(v * qs, fp8_max);
+#ifdef PCAMD_SOFTWARE_FP8_CONVERT
+  return sw_encode<FMT>(q);
+#else
+  return hw_pack4<FMT>(q, 0.0f, 0.0f, 0.0f) & 0xFFu;
+#endif
+}
+
+// Scale formulas of the reference kernels (IEEE fp32 division).
+// per-block:   dequant = 1 / (fp8_max / max(amax, eps))
+// per-channel: dequant = max(amax, eps) / fp8_max
+// per-tensor:  dequant = 1 / ((1 / max(amax, eps)) * fp8_max)
+struct Scales {
+  float qs, ds;
+};
+PCAMD_DEV Scales block_scales(float amax, float fp8_max, float eps) {
+  float s = fmaxf(amax, eps);
+  float qs = fp8_max / s;
+  return {qs, 1.0f / qs};
+}
+PCAMD_DEV Scales channel_scales(float amax, float fp8_max, float eps) {
+  float s = fmaxf(amax, eps);
+  return {fp8_max / s, s / fp8_max};
+}
+// per-tensor: the reference evaluates `fp8_max / max_abs` as a torch tensor
+// op, i.e. reciprocal(max_abs) * fp8_max (two roundings), then reciprocal.
+PCAMD_DEV Scales tensor_scales(float amax, float fp8_max, float eps) {
+  float s = fmaxf(amax, eps);
+  float qs = (1.0f / s) * fp8_max;
+  return {qs, 1.0f / qs};
+}
+
+}  // namespace pcamd

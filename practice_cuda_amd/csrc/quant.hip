@@ -1,0 +1,736 @@
+// quant.hip - gfx950 FP8 quantizers behind the C ABI (include/pcamd_fp8.h).
+//
+// Kernels (all HBM-bound; each element is read once from HBM):
+//   quant_rows_kernel   row-contiguous input; every lane owns an 8-element
+//                       chunk (one 128-bit load for bf16/fp16). Groups of
+//                       LPG lanes share a scale (per-block 1 x 8*LPG), or the
+//                       whole row held in registers shares one (per-channel,
+//                       channel_axis = -2). Amax via DPP inside the wave.
+//   quant_tile_kernel   one workgroup per block_m x block_n block held in
+//                       registers (e.g. 128 x 128 = 8 chunks per thread);
+//                       wave DPP max, then an LDS max across the 4 waves.
+//   quant_cols_kernel   row-contiguous input with column groups (block_n = 1,
+//                       16 <= block_m <= 256, held in registers) or whole
+//                       columns (channel_axis = -1, two passes over the strip).
+//   quant_*_generic     any strides / block shape; one workgroup per block or
+//                       channel, two passes (second read served by L2).
+//   per-tensor          amax kernel (workgroup max + one atomic max on the
+//                       fp32 bit pattern), quantize kernel, finalize kernel.
+//
+// Reference semantics (xuOAO/practice_cuda):
+//   kernels/quant/per_block.py:35-48, kernels/quant/per_channel.py:136-267,
+//   impls/triton_per_tensor.py:40-44 + kernels/quant/per_tensor.py:36-43.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdint>
+
+#include "abi_util.h"
+#include "fp8_common.h"
+
+namespace pcamd {
+
+constexpr int kThreads = 256;
+constexpr int kMaxSlots = 16;  // chunk slots held in registers per lane
+
+// ===========================================================================
+// row-contiguous kernel
+// ===========================================================================
+struct RowArgs {
+  const char* x;
+  uint8_t* y;
+  float* scale;
+  int64_t m;      // rows per batch
+  int64_t sxb, sxm;  // input strides (elements)
+  int64_t syb, sym;  // output strides (bytes == elements)
+  int64_t ssb, ssm, ssn;  // scale strides (elements)
+  int64_t units;  // rows * segs
+  int32_t chunks; // 8-element chunks per row
+  int32_t cpl;    // chunk slots per lane per segment (<= kMaxSlots)
+  int32_t segs;   // segments per row
+  float fp8_max, eps;
+};
+
+template <int DT, int FMT, int LPG, bool WHOLE_ROW>
+__global__ __launch_bounds__(kThreads) void quant_rows_kernel(RowArgs a) {
+  constexpr int EB = elem_bytes<DT>();
+  const int lane = threadIdx.x & 63;
+  const int64_t nwaves = static_cast<int64_t>(gridDim.x) * (kThreads / 64);
+  for (int64_t u = static_cast<int64_t>(blockIdx.x) * (kThreads / 64) + (threadIdx.x >> 6);
+       u < a.units; u += nwaves) {
+    const int64_t row = u / a.segs;
+    const int seg = static_cast<int>(u - row * a.segs);
+    const int64_t b = row / a.m;
+    const int64_t mi = row - b * a.m;
+    const char* xrow = a.x + (b * a.sxb + mi * a.sxm) * EB;
+    uint8_t* yrow = a.y + b * a.syb + mi * a.sym;
+    const int chunk0 = seg * a.cpl * 64 + lane;
+
+    Chunk<DT> raw[kMaxSlots];
+#pragma unroll
+    for (int c = 0; c < kMaxSlots; ++c) {
+      if (c < a.cpl) {
+        const int ch = chunk0 + c * 64;
+        if (ch < a.chunks) load_chunk<DT>(raw[c], xrow + static_cast<int64_t>(ch) * 8 * EB);
+        else zero_chunk<DT>(raw[c]);
+      }
+    }
+
+    if constexpr (WHOLE_ROW) {
+      // one segment per row (host guarantees segs == 1): one scale per row
+      float amax = 0.0f;
+#pragma unroll
+      for (int c = 0; c < kMaxSlots; ++c)
+        if (c < a.cpl) amax = fmaxf(amax, chunk_amax<DT>(raw[c]));
+      amax = group_max<64>(amax);
+      const Scales s = channel_scales(amax, a.fp8_max, a.eps);
+      if (lane == 0) a.scale[b * a.ssb + mi * a.ssm] = s.ds;
+#pragma unroll
+      for (int c = 0; c < kMaxSlots; ++c) {
+        const int ch = chunk0 + c * 64;
+        if (c < a.cpl && ch < a.chunks)
+          *reinterpret_cast<uint2*>(yrow + static_cast<int64_t>(ch) * 8) =
+              quant_chunk<DT, FMT>(raw[c], s.qs, a.fp8_max);
+      }
+    } else {
+#pragma unroll
+      for (int c = 0; c < kMaxSlots; ++c) {
+        if (c < a.cpl) {
+          const int ch = chunk0 + c * 64;
+          const float amax = group_max<LPG>(chunk_amax<DT>(raw[c]));
+          const Scales s = block_scales(amax, a.fp8_max, a.eps);
+          if (ch < a.chunks) {
+            if ((lane & (LPG - 1)) == 0) a.scale[b * a.ssb + mi * a.ssm + (ch / LPG) * a.ssn] = s.ds;
+            *reinterpret_cast<uint2*>(yrow + static_cast<int64_t>(ch) * 8) =
+                quant_chunk<DT, FMT>(raw[c], s.qs, a.fp8_max);
+          }
+        }
+      }
+    }
+  }
+}
+
+// ===========================================================================
+// tile kernel: one workgroup per block_m x block_n block
+// ===========================================================================
+struct TileArgs {
+  const char* x;
+  uint8_t* y;
+  float* scale;
+  int64_t m, n;
+  int64_t sxb, sxm, syb, sym, ssb, ssm, ssn;
+  int64_t mb, nb;    // blocks along m, n
+  int64_t blocks;    // batch * mb * nb
+  int32_t block_m;
+  int32_t cpt;       // chunks per thread = block_m * LPR / 256
+  float fp8_max, eps;
+};
+
+template <int DT, int FMT, int LPR>
+__global__ __launch_bounds__(kThreads) void quant_tile_kernel(TileArgs a) {
+  constexpr int EB = elem_bytes<DT>();
+  constexpr int RPP = kThreads / LPR;  // rows per pass
+  __shared__ float red[kThreads / 64];
+  const int t = threadIdx.x;
+  const int rp = t / LPR, lr = t % LPR;
+  for (int64_t blk = blockIdx.x; blk < a.blocks; blk += gridDim.x) {
+    const int64_t b = blk / (a.mb * a.nb);
+    const int64_t rem = blk - b * a.mb * a.nb;
+    const int64_t pm = rem / a.nb, pn = rem - pm * a.nb;
+    const int64_t r0 = pm * a.block_m;
+    const int64_t col = pn * (LPR * 8) + lr * 8;
+    const char* xb = a.x + (b * a.sxb) * EB;
+    uint8_t* yb = a.y + b * a.syb;
+
+    Chunk<DT> raw[kMaxSlots];
+    float amax = 0.0f;
+#pragma unroll
+    for (int p = 0; p < kMaxSlots; ++p) {
+      if (p < a.cpt) {
+        const int64_t r = r0 + p * RPP + rp;
+        if (r < a.m && col < a.n) {
+          load_chunk<DT>(raw[p], xb + (r * a.sxm + col) * EB);
+        } else {
+          zero_chunk<DT>(raw[p]);
+        }
+      }
+    }
+#pragma unroll
+    for (int p = 0; p < kMaxSlots; ++p)
+      if (p < a.cpt) amax = fmaxf(amax, chunk_amax<DT>(raw[p]));
+    amax = group_max<64>(amax);
+    if ((t & 63) == 0) red[t >> 6] = amax;
+    __syncthreads();
+    amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    __syncthreads();  // red[] is reused by the next block of this workgroup
+    const Scales s = block_scales(amax, a.fp8_max, a.eps);
+    if (t == 0) a.scale[b * a.ssb + pm * a.ssm + pn * a.ssn] = s.ds;
+#pragma unroll
+    for (int p = 0; p < kMaxSlots; ++p) {
+      if (p < a.cpt) {
+        const int64_t r = r0 + p * RPP + rp;
+        if (r < a.m && col < a.n)
+          *reinterpret_cast<uint2*>(yb + r * a.sym + col) = quant_chunk<DT, FMT>(raw[p], s.qs, a.fp8_max);
+      }
+    }
+  }
+}
+
+// ===========================================================================
+// column kernel: 128-column strips, column groups or whole columns
+// ===========================================================================
+struct ColArgs {
+  const char* x;
+  uint8_t* y;
+  float* scale;
+  int64_t m, n;
+  int64_t sxb, sxm, syb, sym;
+  int64_t ssb, ssm, ssn;  // group mode: scale[b, group, col]; channel: scale[b, col] via ssb, ssn
+  int64_t strips;         // ceil(n / 128)
+  int64_t groups;         // row groups per batch (group mode), 1 for channel mode
+  int64_t units;          // batch * groups * strips
+  int32_t group_rows;     // rows per group (group mode)
+  int32_t rpt;            // rows per thread (group mode) = group_rows / 16
+  float fp8_max, eps;
+};
+
+template <int DT, int FMT, bool CHANNEL>
+__global__ __launch_bounds__(kThreads) void quant_cols_kernel(ColArgs a) {
+  constexpr int EB = elem_bytes<DT>();
+  constexpr int SLICES = kThreads / 16;  // 16 threads x 8 columns = 128 columns
+  __shared__ float part[SLICES][128];
+  __shared__ float qsv[128];
+  const int t = threadIdx.x;
+  const int lc = t & 15, rs = t >> 4;
+  for (int64_t u = blockIdx.x; u < a.units; u += gridDim.x) {
+    const int64_t b = u / (a.groups * a.strips);
+    const int64_t rem = u - b * a.groups * a.strips;
+    const int64_t g = rem / a.strips, strip = rem - g * a.strips;
+    const int64_t col = strip * 128 + lc * 8;
+    const bool col_ok = col < a.n;
+    const char* xb = a.x + b * a.sxb * EB;
+    uint8_t* yb = a.y + b * a.syb;
+    float cmax[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+
+    if constexpr (CHANNEL) {
+      for (int64_t r = rs; r < a.m; r += SLICES) {
+        if (col_ok) {
+          Chunk<DT> c;
+          load_chunk<DT>(c, xb + (r * a.sxm + col) * EB);
+          float v[8];
+          unpack_chunk<DT>(c, v);
+#pragma unroll
+          for (int i = 0; i < 8; ++i) cmax[i] = fmaxf(cmax[i], fabsf(v[i]));
+        }
+      }
+    } else {
+      Chunk<DT> raw[kMaxSlots];
+      const int64_t r0 = g * a.group_rows;
+#pragma unroll
+      for (int p = 0; p < kMaxSlots; ++p) {
+        if (p < a.rpt) {
+          const int64_t r = r0 + p * SLICES + rs;
+          if (r < a.m && col_ok) load_chunk<DT>(raw[p], xb + (r * a.sxm + col) * EB);
+          else zero_chunk<DT>(raw[p]);
+          float v[8];
+          unpack_chunk<DT>(raw[p], v);
+#pragma unroll
+          for (int i = 0; i < 8; ++i) cmax[i] = fmaxf(cmax[i], fabsf(v[i]));
+        }
+      }
+      // column maxima across the 16 row slices
+#pragma unroll
+      for (int i = 0; i < 8; ++i) part[rs][lc * 8 + i] = cmax[i];
+      __syncthreads();
+      if (t < 128) {
+        float mx = 0.0f;
+#pragma unroll
+        for (int s = 0; s < SLICES; ++s) mx = fmaxf(mx, part[s][t]);
+        const Scales sc = block_scales(mx, a.fp8_max, a.eps);
+        qsv[t] = sc.qs;
+        const int64_t c = strip * 128 + t;
+        if (c < a.n) a.scale[b * a.ssb + g * a.ssm + c * a.ssn] = sc.ds;
+      }
+      __syncthreads();
+#pragma unroll
+      for (int p = 0; p < kMaxSlots; ++p) {
+        if (p < a.rpt) {
+          const int64_t r = r0 + p * SLICES + rs;
+          if (r < a.m && col_ok) {
+            float v[8];
+            unpack_chunk<DT>(raw[p], v);
+            float q[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) q[i] = clamp_sym(v[i] * qsv[lc * 8 + i], a.fp8_max);
+            *reinterpret_cast<uint2*>(yb + r * a.sym + col) =
+                make_uint2(pack4<FMT>(q[0], q[1], q[2], q[3]), pack4<FMT>(q[4], q[5], q[6], q[7]));
+          }
+        }
+      }
+      __syncthreads();
+      continue;
+    }
+
+    // channel mode: reduce, then a second pass over the strip
+#pragma unroll
+    for (int i = 0; i < 8; ++i) part[rs][lc * 8 + i] = cmax[i];
+    __syncthreads();
+    if (t < 128) {
+      float mx = 0.0f;
+#pragma unroll
+      for (int s = 0; s < SLICES; ++s) mx = fmaxf(mx, part[s][t]);
+      const Scales sc = channel_scales(mx, a.fp8_max, a.eps);
+      qsv[t] = sc.qs;
+      const int64_t c = strip * 128 + t;
+      if (c < a.n) a.scale[b * a.ssb + c * a.ssn] = sc.ds;
+    }
+    __syncthreads();
+    float qs[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) qs[i] = qsv[lc * 8 + i];
+    for (int64_t r = rs; r < a.m; r += SLICES) {
+      if (col_ok) {
+        Chunk<DT> c;
+        load_chunk<DT>(c, xb + (r * a.sxm + col) * EB);
+        float v[8];
+        unpack_chunk<DT>(c, v);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] = clamp_sym(v[i] * qs[i], a.fp8_max);
+        *reinterpret_cast<uint2*>(yb + r * a.sym + col) =
+            make_uint2(pack4<FMT>(v[0], v[1], v[2], v[3]), pack4<FMT>(v[4], v[5], v[6], v[7]));
+      }
+    }
+    __syncthreads();
+  }
+}
+
+// ===========================================================================
+// generic kernels: any strides, any block shape
+// ===========================================================================
+struct GenArgs {
+  const char* x;
+  uint8_t* y;
+  float* scale;
+  int64_t m, n;
+  int64_t sxb, sxm, sxn, syb, sym, syn;
+  int64_t ssb, ssm, ssn;
+  int64_t bm, bn;     // block shape (block mode); channel mode: see kernel
+  int64_t mb, nb;
+  int64_t units;
+  float fp8_max, eps;
+};
+
+PCAMD_DEV float block_reduce_max(float v, float* red) {
+  v = group_max<64>(v);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  v = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  __syncthreads();
+  return v;
+}
+
+// MODE 0: per block (bm x bn); MODE 1: per channel along rows (one row per
+// unit, reduce over n); MODE 2: per channel along columns (reduce over m).
+template <int DT, int FMT, int MODE>
+__global__ __launch_bounds__(kThreads) void quant_generic_kernel(GenArgs a) {
+  __shared__ float red[kThreads / 64];
+  for (int64_t u = blockIdx.x; u < a.units; u += gridDim.x) {
+    int64_t b, r0, r1, c0, c1, pm = 0, pn = 0;
+    if constexpr (MODE == 0) {
+      b = u / (a.mb * a.nb);
+      const int64_t rem = u - b * a.mb * a.nb;
+      pm = rem / a.nb;
+      pn = rem - pm * a.nb;
+      r0 = pm * a.bm; r1 = min(r0 + a.bm, a.m);
+      c0 = pn * a.bn; c1 = min(c0 + a.bn, a.n);
+    } else if constexpr (MODE == 1) {
+      b = u / a.m; pm = u - b * a.m;
+      r0 = pm; r1 = pm + 1; c0 = 0; c1 = a.n;
+    } else {
+      b = u / a.n; pn = u - b * a.n;
+      r0 = 0; r1 = a.m; c0 = pn; c1 = pn + 1;
+    }
+    const int64_t w = c1 - c0;
+    const int64_t cnt = (r1 - r0) * w;
+    float amax = 0.0f;
+    for (int64_t i = threadIdx.x; i < cnt; i += kThreads) {
+      const int64_t r = r0 + i / w, c = c0 + i % w;
+      amax = fmaxf(amax, fabsf(load_one<DT>(a.x, b * a.sxb + r * a.sxm + c * a.sxn)));
+    }
+    amax = block_reduce_max(amax, red);
+    const Scales s = MODE == 0 ? block_scales(amax, a.fp8_max, a.eps)
+                               : channel_scales(amax, a.fp8_max, a.eps);
+    if (threadIdx.x == 0) {
+      if constexpr (MODE == 0) a.scale[b * a.ssb + pm * a.ssm + pn * a.ssn] = s.ds;
+      else if constexpr (MODE == 1) a.scale[b * a.ssb + pm * a.ssm] = s.ds;
+      else a.scale[b * a.ssb + pn * a.ssn] = s.ds;
+    }
+    for (int64_t i = threadIdx.x; i < cnt; i += kThreads) {
+      const int64_t r = r0 + i / w, c = c0 + i % w;
+      const float v = load_one<DT>(a.x, b * a.sxb + r * a.sxm + c * a.sxn);
+      a.y[b * a.syb + r * a.sym + c * a.syn] = static_cast<uint8_t>(quant_one<DT, FMT>(v, s.qs, a.fp8_max));
+    }
+  }
+}
+
+// ===========================================================================
+// per-tensor
+// ===========================================================================
+__global__ void fill_zero_u32_kernel(uint32_t* p) { *p = 0u; }
+
+struct TensorArgs {
+  const char* x;
+  uint8_t* y;
+  float* scale;        // holds amax bits between the kernels, then 1 / qs
+  float* quant_scale;  // optional
+  int64_t batch, m, n;
+  int64_t sxb, sxm, sxn, syb, sym, syn;
+  int64_t total;       // batch * m * n
+  float fp8_max, eps;
+};
+
+template <int DT>
+__global__ __launch_bounds__(kThreads) void tensor_amax_kernel(TensorArgs a) {
+  __shared__ float red[kThreads / 64];
+  float amax = 0.0f;
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * kThreads;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x; i < a.total; i += stride) {
+    const int64_t b = i / (a.m * a.n);
+    const int64_t rem = i - b * a.m * a.n;
+    const int64_t r = rem / a.n, c = rem - r * a.n;
+    amax = fmaxf(amax, fabsf(load_one<DT>(a.x, b * a.sxb + r * a.sxm + c * a.sxn)));
+  }
+  amax = block_reduce_max(amax, red);
+  // non-negative fp32 order equals uint32 order of the bit patterns
+  if (threadIdx.x == 0) atomicMax(reinterpret_cast<uint32_t*>(a.scale), __float_as_uint(amax));
+}
+
+template <int DT, int FMT>
+__global__ __launch_bounds__(kThreads) void tensor_quant_kernel(TensorArgs a) {
+  const float amax = __uint_as_float(*reinterpret_cast<const uint32_t*>(a.scale));
+  const Scales s = tensor_scales(amax, a.fp8_max, a.eps);
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * kThreads;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x; i < a.total; i += stride) {
+    const int64_t b = i / (a.m * a.n);
+    const int64_t rem = i - b * a.m * a.n;
+    const int64_t r = rem / a.n, c = rem - r * a.n;
+    const float v = load_one<DT>(a.x, b * a.sxb + r * a.sxm + c * a.sxn);
+    a.y[b * a.syb + r * a.sym + c * a.syn] = static_cast<uint8_t>(quant_one<DT, FMT>(v, s.qs, a.fp8_max));
+  }
+}
+
+__global__ void tensor_finalize_kernel(TensorArgs a) {
+  const float amax = __uint_as_float(*reinterpret_cast<const uint32_t*>(a.scale));
+  const Scales s = tensor_scales(amax, a.fp8_max, a.eps);
+  *a.scale = s.ds;
+  if (a.quant_scale) *a.quant_scale = s.qs;
+}
+
+// ===========================================================================
+// conversion self-test
+// ===========================================================================
+template <int FMT>
+__global__ __launch_bounds__(kThreads) void selftest_convert_kernel(uint32_t* result, uint32_t limit) {
+  // Every pattern p in [0, limit] (limit = bits of the fp8 max) is converted
+  // in lane position 0 of a packed quadruple (x, y, -x, w) with y and w drawn
+  // from other patterns of the range, so sign handling and the byte order of
+  // the packed result are checked along with the rounding.
+  uint32_t bad = 0, first = 0xFFFFFFFFu;
+  const uint32_t stride = gridDim.x * kThreads;
+  for (uint32_t p = blockIdx.x * kThreads + threadIdx.x; p <= limit; p += stride) {
+    const float x = __uint_as_float(p);
+    const float y = -__uint_as_float(limit - p);
+    const float w = (p ^ 1u) <= limit ? __uint_as_float(p ^ 1u) : 0.0f;
+    const uint32_t hw = hw_pack4<FMT>(x, y, -x, w);
+    const uint32_t sw = sw_encode<FMT>(x) | (sw_encode<FMT>(y) << 8) | (sw_encode<FMT>(-x) << 16) |
+                        (sw_encode<FMT>(w) << 24);
+    if (hw != sw) {
+      ++bad;
+      first = min(first, p);
+    }
+  }
+  if (bad) {
+    atomicAdd(&result[0], bad);
+    atomicMin(&result[1], first);
+  }
+  if (blockIdx.x == 0 && threadIdx.x == 0) atomicAdd(&result[2], limit + 1u);
+}
+
+__global__ void selftest_init_kernel(uint32_t* result) {
+  result[0] = 0u;
+  result[1] = 0xFFFFFFFFu;
+  result[2] = 0u;
+  result[3] = 0u;
+}
+
+// ===========================================================================
+// host dispatch helpers
+// ===========================================================================
+inline int grid_for(int64_t units, int64_t per_block = 1, int64_t cap = 1 << 20) {
+  int64_t g = (units + per_block - 1) / per_block;
+  return static_cast<int>(std::max<int64_t>(1, std::min<int64_t>(g, cap)));
+}
+
+template <template <int, int> class Launch, typename... Args>
+int dispatch_dt_fmt(int dt, int fmt, Args&&... args) {
+  if (fmt == kE4M3) {
+    if (dt == kBF16) return Launch<kBF16, kE4M3>::run(args...);
+    if (dt == kF16) return Launch<kF16, kE4M3>::run(args...);
+    return Launch<kF32, kE4M3>::run(args...);
+  }
+  if (dt == kBF16) return Launch<kBF16, kE5M2>::run(args...);
+  if (dt == kF16) return Launch<kF16, kE5M2>::run(args...);
+  return Launch<kF32, kE5M2>::run(args...);
+}
+
+template <int DT, int FMT>
+struct LaunchRows {
+  static int run(const RowArgs& a, int lpg, bool whole_row, hipStream_t st) {
+    const int grid = grid_for(a.units, kThreads / 64);
+    if (whole_row) {
+      quant_rows_kernel<DT, FMT, 64, true><<<grid, kThreads, 0, st>>>(a);
+    } else {
+      switch (lpg) {
+        case 1: quant_rows_kernel<DT, FMT, 1, false><<<grid, kThreads, 0, st>>>(a); break;
+        case 2: quant_rows_kernel<DT, FMT, 2, false><<<grid, kThreads, 0, st>>>(a); break;
+        case 4: quant_rows_kernel<DT, FMT, 4, false><<<grid, kThreads, 0, st>>>(a); break;
+        case 8: quant_rows_kernel<DT, FMT, 8, false><<<grid, kThreads, 0, st>>>(a); break;
+        case 16: quant_rows_kernel<DT, FMT, 16, false><<<grid, kThreads, 0, st>>>(a); break;
+        case 32: quant_rows_kernel<DT, FMT, 32, false><<<grid, kThreads, 0, st>>>(a); break;
+        case 64: quant_rows_kernel<DT, FMT, 64, false><<<grid, kThreads, 0, st>>>(a); break;
+        default: return set_error(PCAMD_ERR_UNSUPPORTED, "row kernel: unsupported lanes per group %d", lpg);
+      }
+    }
+    return check_launch("quant_rows_kernel");
+  }
+};
+
+template <int DT, int FMT>
+struct LaunchTile {
+  static int run(const TileArgs& a, int lpr, hipStream_t st) {
+    const int grid = grid_for(a.blocks);
+    switch (lpr) {
+      case 4: quant_tile_kernel<DT, FMT, 4><<<grid, kThreads, 0, st>>>(a); break;
+      case 8: quant_tile_kernel<DT, FMT, 8><<<grid, kThreads, 0, st>>>(a); break;
+      case 16: quant_tile_kernel<DT, FMT, 16><<<grid, kThreads, 0, st>>>(a); break;
+      case 32: quant_tile_kernel<DT, FMT, 32><<<grid, kThreads, 0, st>>>(a); break;
+      case 64: quant_tile_kernel<DT, FMT, 64><<<grid, kThreads, 0, st>>>(a); break;
+      default: return set_error(PCAMD_ERR_UNSUPPORTED, "tile kernel: unsupported lanes per row %d", lpr);
+    }
+    return check_launch("quant_tile_kernel");
+  }
+};
+
+template <int DT, int FMT>
+struct LaunchCols {
+  static int run(const ColArgs& a, bool channel, hipStream_t st) {
+    const int grid = grid_for(a.units);
+    if (channel) quant_cols_kernel<DT, FMT, true><<<grid, kThreads, 0, st>>>(a);
+    else quant_cols_kernel<DT, FMT, false><<<grid, kThreads, 0, st>>>(a);
+    return check_launch("quant_cols_kernel");
+  }
+};
+
+template <int DT, int FMT>
+struct LaunchGeneric {
+  static int run(const GenArgs& a, int mode, hipStream_t st) {
+    const int grid = grid_for(a.units);
+    if (mode == 0) quant_generic_kernel<DT, FMT, 0><<<grid, kThreads, 0, st>>>(a);
+    else if (mode == 1) quant_generic_kernel<DT, FMT, 1><<<grid, kThreads, 0, st>>>(a);
+    else quant_generic_kernel<DT, FMT, 2><<<grid, kThreads, 0, st>>>(a);
+    return check_launch("quant_generic_kernel");
+  }
+};
+
+template <int DT, int FMT>
+struct LaunchTensor {
+  static int run(const TensorArgs& a, hipStream_t st) {
+    fill_zero_u32_kernel<<<1, 1, 0, st>>>(reinterpret_cast<uint32_t*>(a.scale));
+    const int grid = grid_for(a.total, kThreads, 4096);
+    if (a.total > 0) tensor_amax_kernel<DT><<<grid, kThreads, 0, st>>>(a);
+    if (a.total > 0) tensor_quant_kernel<DT, FMT><<<grid, kThreads, 0, st>>>(a);
+    tensor_finalize_kernel<<<1, 1, 0, st>>>(a);
+    return check_launch("per-tensor kernels");
+  }
+};
+
+inline bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+inline bool is_pow2(int64_t v) { return v > 0 && (v & (v - 1)) == 0; }
+
+// row-contiguous fast-path eligibility: unit element stride, rows made of
+// whole 8-element chunks, 16-byte aligned input chunks, 8-byte output chunks
+inline bool row_fast_ok(const void* x, int dt, const void* y, int64_t n, int64_t sxb, int64_t sxm,
+                        int64_t sxn, int64_t syb, int64_t sym, int64_t syn) {
+  const int64_t vec = dt == kF32 ? 4 : 8;  // elements per 16 bytes
+  return sxn == 1 && syn == 1 && n % 8 == 0 && aligned(x, 16) && aligned(y, 8) && sxb % vec == 0 &&
+         sxm % vec == 0 && syb % 8 == 0 && sym % 8 == 0;
+}
+
+int validate_common(const void* x, int x_dtype, int64_t batch, int64_t m, int64_t n, const void* y,
+                    int y_dtype, const void* scale, float fp8_max) {
+  if (x_dtype != kF32 && x_dtype != kBF16 && x_dtype != kF16)
+    return set_error(PCAMD_ERR_INVALID, "unsupported input dtype code %d", x_dtype);
+  if (y_dtype != kE4M3 && y_dtype != kE5M2)
+    return set_error(PCAMD_ERR_INVALID, "unsupported fp8 dtype code %d", y_dtype);
+  if (batch < 0 || m < 0 || n < 0) return set_error(PCAMD_ERR_INVALID, "negative size");
+  if (!(fp8_max > 0.0f)) return set_error(PCAMD_ERR_INVALID, "fp8_max must be positive");
+  if (batch * m * n > 0 && (!x || !y || !scale)) return set_error(PCAMD_ERR_INVALID, "null pointer");
+  return PCAMD_OK;
+}
+
+}  // namespace pcamd
+
+using namespace pcamd;
+
+extern "C" int pcamd_quant_block(const void* x, int x_dtype, int64_t batch, int64_t m, int64_t n,
+                                 int64_t sxb, int64_t sxm, int64_t sxn, void* y, int y_dtype,
+                                 int64_t syb, int64_t sym, int64_t syn, float* scale, int64_t ssb,
+                                 int64_t ssm, int64_t ssn, int64_t block_m, int64_t block_n,
+                                 float fp8_max, float eps, void* stream) {
+  clear_error();
+  int rc = validate_common(x, x_dtype, batch, m, n, y, y_dtype, scale, fp8_max);
+  if (rc) return rc;
+  if (!is_pow2(block_m) || !is_pow2(block_n))
+    return set_error(PCAMD_ERR_INVALID, "block sizes must be powers of two, got %lld x %lld",
+                     (long long)block_m, (long long)block_n);
+  if (batch == 0 || m == 0 || n == 0) return PCAMD_OK;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const bool fast = row_fast_ok(x, x_dtype, y, n, sxb, sxm, sxn, syb, sym, syn);
+  const int64_t mb = (m + block_m - 1) / block_m, nb = (n + block_n - 1) / block_n;
+
+  if (fast && block_m == 1 && block_n >= 8 && block_n <= 512) {
+    RowArgs a{};
+    a.x = static_cast<const char*>(x); a.y = static_cast<uint8_t*>(y); a.scale = scale;
+    a.m = m; a.sxb = sxb; a.sxm = sxm; a.syb = syb; a.sym = sym;
+    a.ssb = ssb; a.ssm = ssm; a.ssn = ssn;
+    a.chunks = static_cast<int32_t>(n / 8);
+    const int lpg = static_cast<int>(block_n / 8);
+    int cpl = static_cast<int>(std::min<int64_t>(kMaxSlots, (a.chunks + 63) / 64));
+    cpl = std::max(cpl, 1);
+    a.cpl = cpl;
+    a.segs = static_cast<int32_t>((a.chunks + 64LL * cpl - 1) / (64LL * cpl));
+    a.units = batch * m * a.segs;
+    a.fp8_max = fp8_max; a.eps = eps;
+    if (n / 8 > INT32_MAX) return set_error(PCAMD_ERR_UNSUPPORTED, "row too long");
+    return dispatch_dt_fmt<LaunchRows>(x_dtype, y_dtype, a, lpg, false, st);
+  }
+  const int64_t lpr = block_n / 8;
+  if (fast && block_n >= 32 && lpr <= 64 && (block_m * lpr) % kThreads == 0 &&
+      block_m * lpr / kThreads <= kMaxSlots) {
+    TileArgs a{};
+    a.x = static_cast<const char*>(x); a.y = static_cast<uint8_t*>(y); a.scale = scale;
+    a.m = m; a.n = n; a.sxb = sxb; a.sxm = sxm; a.syb = syb; a.sym = sym;
+    a.ssb = ssb; a.ssm = ssm; a.ssn = ssn; a.mb = mb; a.nb = nb; a.blocks = batch * mb * nb;
+    a.block_m = static_cast<int32_t>(block_m);
+    a.cpt = static_cast<int32_t>(block_m * lpr / kThreads);
+    a.fp8_max = fp8_max; a.eps = eps;
+    return dispatch_dt_fmt<LaunchTile>(x_dtype, y_dtype, a, static_cast<int>(lpr), st);
+  }
+  if (fast && block_n == 1 && block_m >= 16 && block_m <= 256) {
+    ColArgs a{};
+    a.x = static_cast<const char*>(x); a.y = static_cast<uint8_t*>(y); a.scale = scale;
+    a.m = m; a.n = n; a.sxb = sxb; a.sxm = sxm; a.syb = syb; a.sym = sym;
+    a.ssb = ssb; a.ssm = ssm; a.ssn = ssn;
+    a.strips = (n + 127) / 128; a.groups = mb; a.units = batch * mb * a.strips;
+    a.group_rows = static_cast<int32_t>(block_m);
+    a.rpt = static_cast<int32_t>(block_m / 16);
+    a.fp8_max = fp8_max; a.eps = eps;
+    return dispatch_dt_fmt<LaunchCols>(x_dtype, y_dtype, a, false, st);
+  }
+  GenArgs a{};
+  a.x = static_cast<const char*>(x); a.y = static_cast<uint8_t*>(y); a.scale = scale;
+  a.m = m; a.n = n; a.sxb = sxb; a.sxm = sxm; a.sxn = sxn; a.syb = syb; a.sym = sym; a.syn = syn;
+  a.ssb = ssb; a.ssm = ssm; a.ssn = ssn; a.bm = block_m; a.bn = block_n; a.mb = mb; a.nb = nb;
+  a.units = batch * mb * nb; a.fp8_max = fp8_max; a.eps = eps;
+  return dispatch_dt_fmt<LaunchGeneric>(x_dtype, y_dtype, a, 0, st);
+}
+
+extern "C" int pcamd_quant_channel(const void* x, int x_dtype, int64_t batch, int64_t m, int64_t n,
+                                   int64_t sxb, int64_t sxm, int64_t sxn, void* y, int y_dtype,
+                                   int64_t syb, int64_t sym, int64_t syn, float* scale, int64_t ssb,
+                                   int64_t ssc, int channel_axis, float fp8_max, float eps,
+                                   void* stream) {
+  clear_error();
+  int rc = validate_common(x, x_dtype, batch, m, n, y, y_dtype, scale, fp8_max);
+  if (rc) return rc;
+  if (channel_axis != -1 && channel_axis != -2)
+    return set_error(PCAMD_ERR_INVALID, "channel_axis must be -1 or -2, got %d", channel_axis);
+  const int64_t channels = channel_axis == -2 ? m : n;
+  if (batch == 0 || channels == 0) return PCAMD_OK;
+  if (!scale) return set_error(PCAMD_ERR_INVALID, "null scale pointer");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const bool fast = row_fast_ok(x, x_dtype, y, n, sxb, sxm, sxn, syb, sym, syn);
+  if (channel_axis == -2 && n == 0) {
+    // empty reduction: every row scale is eps / fp8_max (nothing to quantize)
+    GenArgs a{};
+    a.x = static_cast<const char*>(x); a.y = static_cast<uint8_t*>(y); a.scale = scale;
+    a.m = m; a.n = 0; a.ssb = ssb; a.ssm = ssc; a.units = batch * m;
+    a.fp8_max = fp8_max; a.eps = eps;
+    return dispatch_dt_fmt<LaunchGeneric>(x_dtype, y_dtype, a, 1, st);
+  }
+  if (channel_axis == -1 && m == 0) {
+    GenArgs a{};
+    a.x = static_cast<const char*>(x); a.y = static_cast<uint8_t*>(y); a.scale = scale;
+    a.m = 0; a.n = n; a.ssb = ssb; a.ssn = ssc; a.units = batch * n;
+    a.fp8_max = fp8_max; a.eps = eps;
+    return dispatch_dt_fmt<LaunchGeneric>(x_dtype, y_dtype, a, 2, st);
+  }
+  if (channel_axis == -2 && fast && n / 8 <= 64LL * kMaxSlots) {
+    RowArgs a{};
+    a.x = static_cast<const char*>(x); a.y = static_cast<uint8_t*>(y); a.scale = scale;
+    a.m = m; a.sxb = sxb; a.sxm = sxm; a.syb = syb; a.sym = sym;
+    a.ssb = ssb; a.ssm = ssc; a.ssn = 0;
+    a.chunks = static_cast<int32_t>(n / 8);
+    a.cpl = std::max(1, static_cast<int>((a.chunks + 63) / 64));
+    a.segs = 1;
+    a.units = batch * m;
+    a.fp8_max = fp8_max; a.eps = eps;
+    return dispatch_dt_fmt<LaunchRows>(x_dtype, y_dtype, a, 64, true, st);
+  }
+  if (channel_axis == -1 && fast) {
+    ColArgs a{};
+    a.x = static_cast<const char*>(x); a.y = static_cast<uint8_t*>(y); a.scale = scale;
+    a.m = m; a.n = n; a.sxb = sxb; a.sxm = sxm; a.syb = syb; a.sym = sym;
+    a.ssb = ssb; a.ssm = 0; a.ssn = ssc;
+    a.strips = (n + 127) / 128; a.groups = 1; a.units = batch * a.strips;
+    a.group_rows = static_cast<int32_t>(std::min<int64_t>(m, INT32_MAX)); a.rpt = 0;
+    a.fp8_max = fp8_max; a.eps = eps;
+    return dispatch_dt_fmt<LaunchCols>(x_dtype, y_dtype, a, true, st);
+  }
+  GenArgs a{};
+  a.x = static_cast<const char*>(x); a.y = static_cast<uint8_t*>(y); a.scale = scale;
+  a.m = m; a.n = n; a.sxb = sxb; a.sxm = sxm; a.sxn = sxn; a.syb = syb; a.sym = sym; a.syn = syn;
+  a.ssb = ssb;
+  if (channel_axis == -2) { a.ssm = ssc; a.units = batch * m; }
+  else { a.ssn = ssc; a.units = batch * n; }
+  a.fp8_max = fp8_max; a.eps = eps;
+  return dispatch_dt_fmt<LaunchGeneric>(x_dtype, y_dtype, a, channel_axis == -2 ? 1 : 2, st);
+}
+
+extern "C" int pcamd_quant_tensor(const void* x, int x_dtype, int64_t batch, int64_t m, int64_t n,
+                                  int64_t sxb, int64_t sxm, int64_t sxn, void* y, int y_dtype,
+                                  int64_t syb, int64_t sym, int64_t syn, float* scale,
+                                  float* quant_scale_out, float fp8_max, float eps, void* stream) {
+  clear_error();
+  int rc = validate_common(x, x_dtype, batch, m, n, y, y_dtype, scale, fp8_max);
+  if (rc) return rc;
+  if (!scale) return set_error(PCAMD_ERR_INVALID, "null scale pointer");
+  TensorArgs a{};
+  a.x = static_cast<const char*>(x); a.y = static_cast<uint8_t*>(y); a.scale = scale;
+  a.quant_scale = quant_scale_out;
+  a.batch = batch; a.m = m; a.n = n; a.sxb = sxb; a.sxm = sxm; a.sxn = sxn;
+  a.syb = syb; a.sym = sym; a.syn = syn; a.total = batch * m * n;
+  a.fp8_max = fp8_max; a.eps = eps;
+  return dispatch_dt_fmt<LaunchTensor>(x_dtype, y_dtype, a, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int pcamd_selftest_fp8_convert(int fmt, uint32_t* result, void* stream) {
+  clear_error();
+  if (!result) return set_error(PCAMD_ERR_INVALID, "null result pointer");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  selftest_init_kernel<<<1, 1, 0, st>>>(result);
+  if (fmt == kE4M3) selftest_convert_kernel<kE4M3><<<4096, kThreads, 0, st>>>(result, 0x43E00000u);
+  else if (fmt == kE5M2) selftest_convert_kernel<kE5M2><<<4096, kThreads, 0, st>>>(result, 0x47600000u);
+  else return set_error(PCAMD_ERR_INVALID, "unknown fp8 format %d", fmt);
+  return check_launch("selftest_convert_kernel");
+}

@@ -1,0 +1,192 @@
+"""Per-block (1 x 128, 128 x 128, any power-of-two) FP8 quantizer and BMM.
+
+Drop-in for fp8_training/fp8_bench/impls/triton_per_block.py of
+xuOAO/practice_cuda: ``hip_per_block_quant`` mirrors ``triton_per_block_quant``
+(:60-150) and ``hip_per_block_bmm`` mirrors ``triton_per_block_bmm``
+(:232-420), with the same arguments, output layouts, metadata and
+ValueErrors; the work runs in the gfx950 kernels of csrc/quant.hip and
+csrc/bmm.hip through the C ABI. ``profile`` and ``use_tma`` are accepted for
+signature compatibility; there is no autotuner to bypass and no TMA unit.
+"""
+from __future__ import annotations
+
+from functools import partial
+from typing import Optional
+
+import torch
+
+from .. import _lib
+from ..registry import QuantResult, register_bmm, register_quant
+from . import _common as C
+
+_DEFAULT_QUANT_BLOCK_M = 128
+_DEFAULT_QUANT_BLOCK_K = 128
+_DEFAULT_QUANT_BLOCK_N = 128
+
+
+def hip_per_block_quant(
+    x: torch.Tensor,
+    *,
+    block_m: int = _DEFAULT_QUANT_BLOCK_M,
+    block_n: int = _DEFAULT_QUANT_BLOCK_N,
+    fp8_dtype: torch.dtype = torch.float8_e4m3fn,
+    eps: float = 1e-12,
+    profile: bool = False,
+) -> QuantResult:
+    """One fp32 dequant scale per block_m x block_n tile of the last two dims."""
+    del profile
+    if x.ndim not in (2, 3):
+        raise ValueError(f"per-block quant expects a 2D or 3D tensor, got {tuple(x.shape)}")
+    if not C.is_power_of_two(block_m) or not C.is_power_of_two(block_n):
+        raise ValueError(
+            "per-block quant currently requires power-of-two block sizes; "
+            f"got block_m={block_m}, block_n={block_n}")
+    C.check_quant_input(x, fp8_dtype, "per-block quant")
+    _lib.require_gpu_tensor(x, "x")
+
+    output = torch.empty_like(x, dtype=fp8_dtype, memory_format=torch.preserve_format)
+    batch, m, n, xs, ys = C.dims3(x, output)
+    m_blocks = -(-m // block_m)
+    n_blocks = -(-n // block_n)
+    scale_storage = torch.empty((batch, m_blocks, n_blocks), device=x.device, dtype=torch.float32)
+
+    L = _lib.lib()
+    with torch.cuda.device(x.device):
+        rc = L.pcamd_quant_block(
+            _lib.ptr(x), _lib.dtype_code(x.dtype), batch, m, n, *xs,
+            _lib.ptr(output), _lib.dtype_code(fp8_dtype), *ys,
+            _lib.ptr(scale_storage), *scale_storage.stride(),
+            block_m, block_n, float(torch.finfo(fp8_dtype).max), float(eps),
+            _lib.stream_of(x))
+    _lib.check(rc, "pcamd_quant_block")
+
+    dequant_scale = scale_storage.squeeze(0) if x.ndim == 2 else scale_storage
+    return QuantResult(
+        tensor=output,
+        dequant_scale=dequant_scale,
+        impl="hip_per_block",
+        granularity="block",
+        meta={
+            "logical_shape": tuple(x.shape),
+            "fp8_dtype": str(fp8_dtype),
+            "block_m": block_m,
+            "block_n": block_n,
+        },
+    )
+
+
+def _validate_scale(value: QuantResult, *, expected_shape, expected_block_m, expected_block_n,
+                    operand: str) -> None:
+    scale = value.dequant_scale
+    if value.granularity != "block":
+        raise ValueError(f"{operand} must use block granularity, got {value.granularity!r}")
+    if tuple(scale.shape) != expected_shape:
+        raise ValueError(
+            f"{operand} dequant scale must have shape {expected_shape}, got {tuple(scale.shape)}")
+    if scale.dtype != torch.float32:
+        raise ValueError(f"{operand} dequant scale must be float32, got {scale.dtype}")
+    if scale.device != value.tensor.device:
+        raise ValueError(f"{operand} dequant scale must be on {value.tensor.device}, got {scale.device}")
+    if value.meta.get("block_m") != expected_block_m or value.meta.get("block_n") != expected_block_n:
+        raise ValueError(
+            f"{operand} must be quantized with block_m={expected_block_m} "
+            f"and block_n={expected_block_n}, "
+            f"got block_m={value.meta.get('block_m')} and block_n={value.meta.get('block_n')}")
+
+
+def _block_shape(value: QuantResult, operand: str) -> tuple[int, int]:
+    if value.granularity != "block":
+        raise ValueError(f"{operand} must use block granularity, got {value.granularity!r}")
+    bm, bn = value.meta.get("block_m"), value.meta.get("block_n")
+    if not isinstance(bm, int) or not isinstance(bn, int) or bm <= 0 or bn <= 0:
+        raise ValueError(f"{operand} has invalid per-block metadata: block_m={bm}, block_n={bn}")
+    return bm, bn
+
+
+def hip_per_block_bmm(
+    a: QuantResult,
+    b: QuantResult,
+    *,
+    out_dtype: torch.dtype = torch.bfloat16,
+    bias: Optional[torch.Tensor] = None,
+    out: Optional[torch.Tensor] = None,
+    do_transpose_a: bool = False,
+    do_transpose_b: bool = False,
+    profile: bool = False,
+    use_tma: bool = False,
+    activation: str = "none",
+) -> torch.Tensor:
+    """Block-scaled FP8 BMM: per quant-K block, acc += (A_blk @ B_blk) * (sa * sb)."""
+    del profile, use_tma
+    a_tensor, b_tensor, batch, m, n, k = C.prepare_operands(
+        a, b, do_transpose_a, do_transpose_b, activation)
+
+    qbm, qbk = _block_shape(a, "A")
+    b_qbk, qbn = _block_shape(b, "B")
+    if qbk != b_qbk:
+        raise ValueError(f"A and B must use the same K quant block: A={qbk}, B={b_qbk}")
+    if qbk < 128 or qbk % 128 != 0:
+        raise ValueError(
+            "the current per-block BMM configs require quant_block_k >= 128 "
+            f"and divisible by 128, got {qbk}")
+    mb, kb, nb = -(-m // qbm), -(-k // qbk), -(-n // qbn)
+    _validate_scale(a, expected_shape=(batch, mb, kb), expected_block_m=qbm, expected_block_n=qbk,
+                    operand="A")
+    _validate_scale(b, expected_shape=(batch, kb, nb), expected_block_m=qbk, expected_block_n=qbn,
+                    operand="B")
+
+    out = C.prepare_out(out, out_dtype, batch, m, n, a_tensor.device)
+    bias, bias_strides, bias_code = C.check_bias(bias, batch, m, n, a_tensor.device)
+    return C.launch_bmm(
+        a_tensor, b_tensor, out, bias, bias_strides, bias_code,
+        a.dequant_scale, a.dequant_scale.stride(), b.dequant_scale, b.dequant_scale.stride(),
+        _lib.SCALE_BLOCK, False, qbm, qbk, qbn, activation, batch, m, n, k)
+
+
+def _register_block_scheme(quant_impl: str, *, quant_block_m: int, quant_block_k: int,
+                           quant_block_n: int, description: str) -> None:
+    """Register the quantizer and its five BMM layout variants
+    (reference impls/triton_per_block.py:436-521)."""
+    register_quant(
+        quant_impl,
+        partial(hip_per_block_quant, block_m=quant_block_m, block_n=quant_block_k),
+        description,
+    )
+    common = {
+        "quant_impl": quant_impl,
+        "quant_a_kwargs": {"block_m": quant_block_m, "block_n": quant_block_k},
+        "quant_b_kwargs": {"block_m": quant_block_k, "block_n": quant_block_n},
+    }
+    register_bmm(
+        f"{quant_impl}_a_k_b_n", partial(hip_per_block_bmm, do_transpose_b=False),
+        layout="n", prepare_b=lambda v: C.prepare_b_layout(v, "n"),
+        description="Per-block FP8 BMM with an N-major [B,K,N] right operand.", **common)
+    register_bmm(
+        f"{quant_impl}_a_k_b_k", partial(hip_per_block_bmm, do_transpose_b=False),
+        layout="k", prepare_b=lambda v: C.prepare_b_layout(v, "k"),
+        description="Per-block FP8 BMM with a prepacked K-major right operand.", **common)
+    register_bmm(
+        f"{quant_impl}_a_k_b_n_transpose", partial(hip_per_block_bmm, do_transpose_b=True),
+        layout="n", prepare_b=lambda v: C.prepare_b_layout(v, "n"),
+        description="N-major per-block FP8 BMM with packing inside the call.", **common)
+    register_bmm(
+        f"{quant_impl}_a_m_b_n",
+        partial(hip_per_block_bmm, do_transpose_a=False, do_transpose_b=False),
+        a_layout="m", layout="n",
+        prepare_a=lambda v: C.prepare_a_layout(v, "m"), prepare_b=lambda v: C.prepare_b_layout(v, "n"),
+        description="Per-block FP8 BMM with direct M-major A and N-major B operands.", **common)
+    register_bmm(
+        f"{quant_impl}_a_m_transpose_b_n_transpose",
+        partial(hip_per_block_bmm, do_transpose_a=True, do_transpose_b=True),
+        a_layout="m", layout="n",
+        prepare_a=lambda v: C.prepare_a_layout(v, "m"), prepare_b=lambda v: C.prepare_b_layout(v, "n"),
+        description="M-major A and N-major B packed inside the per-block BMM call.", **common)
+
+
+_register_block_scheme(
+    "hip_per_block_1d", quant_block_m=1, quant_block_k=_DEFAULT_QUANT_BLOCK_K, quant_block_n=1,
+    description="1D K-block scale quantization; defaults to 1x128 blocks.")
+_register_block_scheme(
+    "hip_per_block_2d", quant_block_m=_DEFAULT_QUANT_BLOCK_M, quant_block_k=_DEFAULT_QUANT_BLOCK_K,
+    quant_block_n=_DEFAULT_QUANT_BLOCK_N,
+    description="2D block scale quantization; defaults to 128x128 blocks.")

@@ -1,0 +1,89 @@
+"""CPU tests of the C ABI: the library loads, exports every function declared
+in include/pcamd_fp8.h, and rejects bad arguments with a status code and a
+message (no kernel is launched on these paths)."""
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+
+import pytest
+
+from practice_cuda_amd import _lib
+
+HEADER = os.path.join(os.path.dirname(os.path.dirname(__file__)), "include", "pcamd_fp8.h")
+FAKE = ctypes.c_void_p(0x10000)  # never dereferenced: validation fails first
+
+
+def declared_functions() -> list[str]:
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\s*\*?\s*(pcamd_\w+)\s*\(", text, re.M)))
+
+
+def test_library_exports_header_symbols():
+    L = _lib.lib()
+    names = declared_functions()
+    assert len(names) >= 7
+    for name in names:
+        assert hasattr(L, name), f"{name} declared in the header but not exported"
+    assert sorted(_lib.EXPORTED_SYMBOLS) == names
+
+
+def test_abi_version_matches_header():
+    text = open(HEADER).read()
+    version = int(re.search(r"#define PCAMD_ABI_VERSION (\d+)", text).group(1))
+    assert _lib.lib().pcamd_abi_version() == version
+
+
+def _quant_block(**over):
+    args = dict(x=FAKE, xd=_lib.BF16, b=1, m=4, n=256, sxb=0, sxm=256, sxn=1, y=FAKE,
+                yd=_lib.E4M3FN, syb=0, sym=256, syn=1, s=FAKE, ssb=0, ssm=2, ssn=1, bm=1, bn=128,
+                fmax=448.0, eps=1e-12, st=None)
+    args.update(over)
+    return _lib.lib().pcamd_quant_block(*args.values())
+
+
+def test_invalid_arguments_are_rejected():
+    L = _lib.lib()
+    assert _quant_block(xd=7) == -1
+    assert b"input dtype" in L.pcamd_last_error()
+    assert _quant_block(yd=_lib.BF16) == -1
+    assert _quant_block(bm=3) == -1 and b"powers of two" in L.pcamd_last_error()
+    assert _quant_block(m=-1) == -1
+    assert _quant_block(x=None) == -1 and b"null" in L.pcamd_last_error()
+    assert _quant_block(fmax=0.0) == -1
+    # empty tensors are valid and launch nothing
+    assert _quant_block(m=0) == 0 and L.pcamd_last_error() == b""
+    rc = L.pcamd_quant_channel(FAKE, _lib.BF16, 1, 4, 256, 0, 256, 1, FAKE, _lib.E4M3FN, 0, 256, 1,
+                               FAKE, 0, 1, 0, 448.0, 1e-12, None)
+    assert rc == -1 and b"channel_axis" in L.pcamd_last_error()
+
+
+def _bmm(**over):
+    args = dict(a=FAKE, b=FAKE, abd=_lib.E4M3FN, B=1, M=128, N=128, K=128,
+                sab=0, sam=128, sak=1, sbb=0, sbk=128, sbn=1, c=FAKE, cd=_lib.BF16,
+                scb=0, scm=128, scn=1, bias=None, biasd=0, sbb0=0, sbm=0, sbn0=0,
+                sa=FAKE, ssab=0, ssa1=1, ssa2=1, sb=FAKE, ssbb=0, ssb1=1, ssb2=1,
+                mode=_lib.SCALE_BLOCK, saq=0, qbm=1, qbk=128, qbn=128, act=0, st=None)
+    args.update(over)
+    return _lib.lib().pcamd_bmm_scaled(*args.values())
+
+
+@pytest.mark.parametrize("over,msg", [
+    (dict(abd=_lib.BF16), b"fp8"),
+    (dict(cd=9), b"output dtype"),
+    (dict(qbk=64), b"multiple of 128"),
+    (dict(qbk=192), b"multiple of 128"),
+    (dict(act=5), b"activation"),
+    (dict(mode=7), b"scale mode"),
+    (dict(sak=2, sam=2), b"contiguous along K or M"),
+    (dict(scn=2), b"contiguous along N"),
+    (dict(sa=None), b"null"),
+])
+def test_bmm_invalid_arguments(over, msg):
+    assert _bmm(**over) == -1
+    assert msg in _lib.lib().pcamd_last_error()
+
+
+def test_bmm_empty_is_ok():
+    assert _bmm(M=0) == 0

@@ -1,0 +1,200 @@
+"""GPU parity of the HIP scaled FP8 BMM against the CPU oracle.
+
+The oracle is the fp64 product of the dequantized operands (the reference's
+kernel_reference, bench_bmm.py:414-419) followed by bias and activation;
+the bar is max|out - ref| / max|ref| <= 1e-2 (north_star). Cases: every
+scaling scheme x the five registered layouts, unaligned shapes from the
+reference tests, bias / GELU / output dtypes, the BASELINE config-4 shape,
+multi-block quant-K, and the invariants of kernels/fp8_bmm/test/
+fp8_quant_bmm_test.py (zeros, linearity, batch independence, determinism).
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as O
+from practice_cuda_amd import get_bmm, get_quant
+from practice_cuda_amd.impls.hip_per_block import hip_per_block_bmm, hip_per_block_quant
+from practice_cuda_amd.impls.hip_per_tensor import hip_per_tensor_bmm
+from practice_cuda_amd.registry import QuantResult
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-2
+LAYOUTS = ("a_k_b_k", "a_k_b_n", "a_k_b_n_transpose", "a_m_b_n", "a_m_transpose_b_n_transpose")
+SCHEMES = ("hip_per_block_1d", "hip_per_block_2d", "hip_per_channel", "hip_per_tensor")
+
+
+def materialize(t: torch.Tensor, layout: str) -> torch.Tensor:
+    """Same logical tensor, the other dim contiguous (bench_bmm.py:280-288)."""
+    if layout in ("m", "k_of_b"):
+        return t.transpose(-1, -2).contiguous().transpose(-1, -2)
+    return t
+
+
+def run_registered(name, a, b, dev, bias=None, activation="none", out_dtype=torch.bfloat16):
+    impl = get_bmm(name)
+    quant = get_quant(impl.quant_impl)
+    a_in = materialize(a, "m") if impl.a_layout == "m" else a
+    b_in = materialize(b, "k_of_b") if impl.layout == "k" else b
+    qa = impl.prepare_a(quant.fn(a_in.to(dev), **impl.quant_a_kwargs))
+    qb = impl.prepare_b(quant.fn(b_in.to(dev), **impl.quant_b_kwargs))
+    kw = impl.prepare_call_kwargs(qa, qb)
+    out = impl.fn(qa, qb, bias=None if bias is None else bias.to(dev), activation=activation,
+                  out_dtype=out_dtype, **kw)
+    torch.cuda.synchronize()
+    ref = O.bmm_reference(qa.dequantize().double().cpu().numpy(),
+                          qb.dequantize().double().cpu().numpy(),
+                          None if bias is None else bias.double().numpy(), activation)
+    return out, ref
+
+
+def rand(shape, seed, scale=1.0):
+    g = torch.Generator().manual_seed(seed)
+    return (torch.randn(*shape, generator=g) * scale).bfloat16()
+
+
+SHAPES = [(2, 128, 128, 128), (3, 33, 47, 65), (3, 129, 131, 127), (2, 256, 384, 512), (1, 64, 96, 1024)]
+
+
+@pytest.mark.parametrize("scheme", SCHEMES)
+@pytest.mark.parametrize("layout", LAYOUTS)
+@pytest.mark.parametrize("shape", SHAPES)
+def test_bmm_matches_oracle(dev, scheme, layout, shape):
+    b_, m, n, k = shape
+    print(f"bmm {scheme}_{layout} {shape}", flush=True)
+    out, ref = run_registered(f"{scheme}_{layout}", rand((b_, m, k), 1), rand((b_, k, n), 2), dev)
+    assert out.shape == (b_, m, n) and out.dtype == torch.bfloat16
+    err = O.max_abs_rel(out.float().cpu().numpy(), ref)
+    assert err <= TOL, f"max_abs_rel {err}"
+
+
+@pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("activation", ["none", "gelu"])
+def test_bmm_bias_activation_dtypes(dev, out_dtype, activation):
+    bias = rand((2, 96, 80), 3)
+    out, ref = run_registered("hip_per_block_2d_a_k_b_n", rand((2, 96, 256), 4), rand((2, 256, 80), 5),
+                              dev, bias=bias, activation=activation, out_dtype=out_dtype)
+    assert out.dtype == out_dtype
+    assert O.max_abs_rel(out.float().cpu().numpy(), ref) <= TOL
+
+
+def test_bmm_fp8_output_saturates(dev):
+    # reference fp8_quant_bmm_test.py:227-237: fp8 output saturates at +-448
+    a = (rand((1, 64, 128), 6).float() * 4).bfloat16()
+    qa = hip_per_block_quant(a.to(dev), block_m=1, block_n=128)
+    qb = hip_per_block_quant(rand((1, 128, 64), 7).to(dev), block_m=128, block_n=128)
+    out = hip_per_block_bmm(qa, qb, out_dtype=torch.float8_e4m3fn)
+    ref = O.bmm_reference(qa.dequantize().double().cpu().numpy(), qb.dequantize().double().cpu().numpy())
+    v = out.float().cpu().numpy()
+    assert np.isfinite(v).all() and np.abs(v).max() <= 448.0
+    close = np.abs(ref) < 400
+    assert np.allclose(v[close], ref[close], rtol=0.2, atol=0.1)
+
+
+def test_bmm_multi_block_quant_k(dev):
+    # quant_block_k = 256: two 128-wide MFMA steps accumulate before each rescale
+    a, b = rand((2, 100, 512), 8), rand((2, 512, 200), 9)
+    qa = hip_per_block_quant(a.to(dev), block_m=1, block_n=256)
+    qb = hip_per_block_quant(b.to(dev), block_m=256, block_n=128)
+    out = hip_per_block_bmm(qa, qb)
+    ref = O.bmm_reference(qa.dequantize().double().cpu().numpy(), qb.dequantize().double().cpu().numpy())
+    assert O.max_abs_rel(out.float().cpu().numpy(), ref) <= TOL
+
+
+def test_bmm_golden(dev):
+    import os
+    d = np.load(os.path.join(os.path.dirname(__file__), "golden", "bmm_golden.npz"))
+    qa = QuantResult(torch.from_numpy(d["qa"]).view(torch.float8_e4m3fn).to(dev),
+                     torch.from_numpy(d["sa"]).to(dev), "golden", "block", {"block_m": 1, "block_n": 128})
+    qb = QuantResult(torch.from_numpy(d["qb"]).view(torch.float8_e4m3fn).to(dev),
+                     torch.from_numpy(d["sb"]).to(dev), "golden", "block", {"block_m": 128, "block_n": 128})
+    bias = torch.from_numpy(d["bias"].view(np.int16)).view(torch.bfloat16).to(dev)
+    out = hip_per_block_bmm(qa, qb, bias=bias, out_dtype=torch.float32)
+    assert O.max_abs_rel(out.cpu().numpy(), d["expected"]) <= TOL
+
+
+def test_config4_shape(dev):
+    """A [128,2048,128] 1x128, B [128,128,512] 128x128, bf16 out."""
+    g = torch.Generator().manual_seed(0)
+    ah = torch.randn(128, 2048, 128, generator=g).bfloat16()
+    bh = torch.randn(128, 128, 512, generator=g).bfloat16()
+    qa = hip_per_block_quant(ah.to(dev), block_m=1, block_n=128)
+    qb = hip_per_block_quant(bh.to(dev), block_m=128, block_n=128)
+    out = hip_per_block_bmm(qa, qb)
+    torch.cuda.synchronize()
+    assert torch.isfinite(out).all()
+    da, db = qa.dequantize().double().cpu(), qb.dequantize().double().cpu()
+    for bi in (0, 37, 127):
+        ref = O.bmm_reference(da[bi:bi + 1].numpy(), db[bi:bi + 1].numpy())
+        assert O.max_abs_rel(out[bi:bi + 1].float().cpu().numpy(), ref) <= TOL
+
+
+def test_fixed_tile_microbench_points(dev):
+    """fp8_training/microbench/profile_fixed_b_n.py:235-283: one 64x64x128 fp8
+    tile times 0.5, bf16 output, assert_close(2e-2) for a_k_b_k / a_k_b_n / a_m_b_n."""
+    torch.manual_seed(0)
+    a = (torch.randn(64, 128) * 0.25).to(torch.float8_e4m3fn)
+    b = (torch.randn(128, 64) * 0.25).to(torch.float8_e4m3fn)
+    ref = ((a.float() @ b.float()) * 0.5).bfloat16().float()
+    scale = torch.tensor(0.5, device=dev)
+    for a_m, b_k in ((False, True), (False, False), (True, False)):
+        at = a.to(dev)[None]
+        bt = b.to(dev)[None]
+        if a_m:
+            at = at.transpose(-1, -2).contiguous().transpose(-1, -2)
+        if b_k:
+            bt = bt.transpose(-1, -2).contiguous().transpose(-1, -2)
+        qa = QuantResult(at, scale, "t", "tensor")
+        qb = QuantResult(bt, torch.tensor(1.0, device=dev), "t", "tensor")
+        out = hip_per_tensor_bmm(qa, qb, dequant_scale=scale)
+        torch.testing.assert_close(out[0].float().cpu(), ref, rtol=2e-2, atol=2e-2)
+
+
+def _fp8(shape, seed):
+    g = torch.Generator().manual_seed(seed)
+    return (torch.randn(*shape, generator=g) * 0.5).to(torch.float8_e4m3fn)
+
+
+def _tensor_bmm(a, b, s, dev, out_dtype=torch.float32):
+    qa = QuantResult(a.to(dev), torch.tensor(1.0, device=dev), "t", "tensor")
+    qb = QuantResult(b.to(dev), torch.tensor(1.0, device=dev), "t", "tensor")
+    return hip_per_tensor_bmm(qa, qb, dequant_scale=torch.tensor(s, device=dev), out_dtype=out_dtype)
+
+
+def test_zeros(dev):
+    a = torch.zeros(2, 32, 64).to(torch.float8_e4m3fn)
+    b = torch.zeros(2, 64, 32).to(torch.float8_e4m3fn)
+    out = _tensor_bmm(a, b, 1.0, dev)
+    assert not torch.isnan(out).any() and out.abs().max().item() == 0.0
+
+
+def test_scale_linearity(dev):
+    a, b = _fp8((1, 64, 64), 1), _fp8((1, 64, 64), 2)
+    o1 = _tensor_bmm(a, b, 1.0, dev)
+    o2 = _tensor_bmm(a, b, 2.0, dev)
+    assert torch.equal(o2, o1 * 2)  # power-of-two scaling is exact in fp32
+
+
+def test_batch_independence(dev):
+    a, b = _fp8((2, 32, 32), 3), _fp8((2, 32, 32), 4)
+    out = _tensor_bmm(a, b, 1.0, dev)
+    for i in range(2):
+        single = _tensor_bmm(a[i:i + 1], b[i:i + 1], 1.0, dev)
+        assert torch.allclose(out[i], single[0], rtol=1e-3, atol=1e-3)
+
+
+def test_exact_small_integers(dev):
+    # fp8 inputs with small integer values: every product and partial sum is
+    # exact in fp32, so the fp32 output must equal the integer matmul exactly
+    g = torch.Generator().manual_seed(5)
+    a = torch.randint(-4, 5, (2, 48, 256), generator=g).float()
+    b = torch.randint(-4, 5, (2, 256, 40), generator=g).float()
+    out = _tensor_bmm(a.to(torch.float8_e4m3fn), b.to(torch.float8_e4m3fn), 1.0, dev)
+    assert torch.equal(out.cpu(), torch.bmm(a, b))
+
+
+def test_determinism(dev):
+    a, b = _fp8((2, 64, 64), 5), _fp8((2, 64, 64), 6)
+    assert torch.equal(_tensor_bmm(a, b, 1.0, dev, torch.bfloat16), _tensor_bmm(a, b, 1.0, dev, torch.bfloat16))

@@ -1,0 +1,270 @@
+"""GPU parity of the HIP quantizers against the CPU oracle: fp8 bytes and fp32
+scale bit patterns must be identical (the north_star's bit-exact bar).
+
+Covers every kernel path of csrc/quant.hip (row groups, tiles, column groups,
+register-resident rows, column strips, generic strided, per-tensor), the
+BASELINE full-size configs 1-3, the golden vectors, and the edge cases of the
+reference tests (zeros, outliers, ragged shapes, 3D batches, e5m2).
+"""
+from __future__ import annotations
+
+import ctypes
+import json
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as O
+from practice_cuda_amd import _lib
+from practice_cuda_amd.impls.hip_per_block import hip_per_block_quant
+from practice_cuda_amd.impls.hip_per_channel import hip_per_channel_quant
+from practice_cuda_amd.impls.hip_per_tensor import hip_per_tensor_quant
+
+pytestmark = pytest.mark.gpu
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
+FMT = {"e4m3": torch.float8_e4m3fn, "e5m2": torch.float8_e5m2}
+DT = {"bf16": torch.bfloat16, "f16": torch.float16, "f32": torch.float32}
+
+
+def qbits(t: torch.Tensor) -> np.ndarray:
+    return t.contiguous().view(torch.uint8).cpu().numpy()
+
+
+def sbits(t: torch.Tensor) -> np.ndarray:
+    return t.detach().float().cpu().numpy().astype(np.float32).reshape(-1).view(np.uint32)
+
+
+def assert_same(res, q_ref, s_ref, label=""):
+    q = qbits(res.tensor)
+    if not np.array_equal(q, q_ref):
+        bad = np.argwhere(q != q_ref)
+        i = tuple(bad[0])
+        raise AssertionError(f"{label}: {len(bad)} fp8 bytes differ, first at {i}: "
+                             f"gpu {q[i]:#x} oracle {q_ref[i]:#x}")
+    sr = np.asarray(s_ref, np.float32).reshape(-1).view(np.uint32)
+    sg = sbits(res.dequant_scale)
+    if not np.array_equal(sg, sr):
+        bad = np.nonzero(sg != sr)[0]
+        raise AssertionError(f"{label}: {len(bad)} scales differ, first at {bad[0]}: "
+                             f"gpu {sg[bad[0]]:#x} oracle {sr[bad[0]]:#x}")
+
+
+def make_input(shape, dtype, seed, scale=1.0, outliers=0.0):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(*shape, generator=g) * scale
+    if outliers:
+        m = torch.rand(*shape, generator=g) < outliers
+        x[m] *= 50.0
+    return x.to(DT[dtype])
+
+
+# ---------------------------------------------------------------------------
+# hardware fp8 conversion == integer restatement over every in-range fp32
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("fmt", [_lib.E4M3FN, _lib.E5M2])
+def test_hw_convert_selftest(dev, fmt):
+    res = torch.zeros(4, dtype=torch.int32, device=dev)
+    print(f"selftest fmt={fmt}", flush=True)
+    _lib.check(_lib.lib().pcamd_selftest_fp8_convert(fmt, _lib.ptr(res), _lib.stream_of(res)),
+               "selftest")
+    torch.cuda.synchronize()
+    r = res.cpu().numpy().view(np.uint32)
+    assert r[2] > 0x40000000, "self-test did not cover the range"
+    assert r[0] == 0, f"{r[0]} mismatches, first pattern {r[1]:#010x}"
+
+
+# ---------------------------------------------------------------------------
+# golden vectors
+# ---------------------------------------------------------------------------
+def _golden():
+    with open(os.path.join(GOLDEN, "quant_golden.json")) as fh:
+        return json.load(fh)
+
+
+@pytest.mark.parametrize("name", sorted(_golden()))
+def test_golden_vectors(dev, name):
+    meta = _golden()[name]
+    d = np.load(os.path.join(GOLDEN, "quant_golden.npz"))
+    raw = d[f"{name}__x"]
+    if meta["dtype"] == "bf16":
+        x = torch.from_numpy(raw.view(np.int16)).view(torch.bfloat16)
+    elif meta["dtype"] == "f16":
+        x = torch.from_numpy(raw.view(np.float16))
+    else:
+        x = torch.from_numpy(raw)
+    x = x.to(dev)
+    fp8 = FMT[meta["fmt"]]
+    print(f"golden {name}", flush=True)
+    if meta["kind"] == "block":
+        r = hip_per_block_quant(x, block_m=meta["bm"], block_n=meta["bn"], fp8_dtype=fp8)
+    elif meta["kind"] == "channel":
+        r = hip_per_channel_quant(x, channel_axis=meta["axis"], fp8_dtype=fp8)
+    else:
+        r = hip_per_tensor_quant(x, fp8_dtype=fp8)
+    assert_same(r, d[f"{name}__q"], d[f"{name}__scale"], name)
+
+
+# ---------------------------------------------------------------------------
+# per-block: every kernel path
+# ---------------------------------------------------------------------------
+BLOCK_CASES = [
+    # (shape, dtype, block_m, block_n, fmt)     path
+    ((2, 5, 384), "bf16", 1, 128, "e4m3"),      # rows, 1x128
+    ((37, 264), "f32", 1, 128, "e4m3"),         # rows, ragged last group, fp32 input
+    ((3, 100, 520), "f16", 1, 64, "e4m3"),      # rows, 1x64
+    ((7, 1032), "bf16", 1, 8, "e4m3"),          # rows, 1x8 (one lane per group)
+    ((5, 2048), "bf16", 1, 512, "e5m2"),        # rows, 1x512 (whole wave per group)
+    ((9, 9000), "bf16", 1, 128, "e4m3"),        # rows, two segments per row
+    ((256, 384), "bf16", 128, 128, "e4m3"),     # tile
+    ((2, 300, 264), "bf16", 128, 128, "e4m3"),  # tile, ragged blocks
+    ((64, 256), "bf16", 64, 64, "e5m2"),        # tile, 64x64
+    ((128, 512), "f32", 128, 256, "e4m3"),      # tile, 128x256, fp32
+    ((1000, 136), "bf16", 128, 1, "e4m3"),      # column groups, ragged
+    ((2, 512, 264), "f16", 256, 1, "e4m3"),     # column groups, 256x1
+    ((96, 64), "bf16", 16, 1, "e4m3"),          # column groups, 16x1
+    ((200, 300), "bf16", 128, 128, "e4m3"),     # generic (n % 8 != 0)
+    ((33, 70), "f32", 4, 32, "e4m3"),           # generic
+    ((2, 64, 256), "bf16", 2, 128, "e4m3"),     # generic (2x128)
+    ((40, 256), "bf16", 1, 1024, "e4m3"),       # generic (group wider than a wave)
+    ((50, 64), "bf16", 8, 1, "e4m3"),           # generic (8x1)
+    ((3, 17, 33), "f16", 1, 1, "e5m2"),         # generic (1x1)
+]
+
+
+@pytest.mark.parametrize("shape,dtype,bm,bn,fmt", BLOCK_CASES)
+def test_block_quant_matches_oracle(dev, shape, dtype, bm, bn, fmt):
+    x = make_input(shape, dtype, seed=hash((shape, bm, bn)) & 0xFFFF, scale=0.5, outliers=0.002)
+    print(f"block {shape} {dtype} {bm}x{bn} {fmt}", flush=True)
+    r = hip_per_block_quant(x.to(dev), block_m=bm, block_n=bn, fp8_dtype=FMT[fmt])
+    q_ref, s_ref = O.quant_block(x, bm, bn, fmt, threads=8)
+    assert r.dequant_scale.shape == s_ref.shape
+    assert r.tensor.dtype == FMT[fmt] and r.tensor.shape == x.shape
+    assert_same(r, q_ref, s_ref, f"{shape} {bm}x{bn}")
+
+
+def test_block_quant_strided_input(dev):
+    # an M-major (transposed) input goes through the generic strided kernel and
+    # keeps its layout in the output (preserve_format)
+    base = make_input((300, 200), "bf16", seed=5).to(dev)
+    x = base.t()
+    r = hip_per_block_quant(x, block_m=1, block_n=128)
+    assert r.tensor.stride() == x.stride()
+    q_ref, s_ref = O.quant_block(x.cpu(), 1, 128)
+    assert_same(r, q_ref, s_ref, "transposed")
+
+
+def test_block_quant_zeros_and_outliers(dev):
+    x = torch.zeros(4, 384, device=dev, dtype=torch.bfloat16)
+    x[1, 5] = -0.0
+    r = hip_per_block_quant(x, block_m=1, block_n=128)
+    q = qbits(r.tensor)
+    assert q[1, 5] == 0x80 and np.count_nonzero(q) == 1
+    assert torch.isfinite(r.dequant_scale).all()
+    y = make_input((64, 64), "f32", seed=6)
+    y[0, 0], y[1, 1] = 1e6, -1e6
+    r = hip_per_block_quant(y.to(dev), block_m=64, block_n=64)
+    q = qbits(r.tensor)
+    assert q[0, 0] == 0x7E and q[1, 1] == 0xFE
+
+
+def test_config1_full_size(dev):
+    """bf16 [4096, 7168], N(0,1) with 0.1% outliers x50, 1x128."""
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(4096, 7168, generator=g)
+    m = torch.rand(4096, 7168, generator=g) < 0.001
+    x[m] *= 50
+    x = x.bfloat16()
+    r = hip_per_block_quant(x.to(dev), block_m=1, block_n=128)
+    q_ref, s_ref = O.quant_block(x, 1, 128, threads=8)
+    assert r.dequant_scale.shape == (4096, 56)
+    assert_same(r, q_ref, s_ref, "config1")
+
+
+def test_config3_full_size(dev):
+    """bf16 [4096, 7168] N(0,0.02) x log-uniform block
+    multipliers in [0.1, 10], 128x128 blocks."""
+    g = torch.Generator().manual_seed(0)
+    w = torch.randn(4096, 7168, generator=g) * 0.02
+    mult = torch.exp(torch.empty(32, 56).uniform_(np.log(0.1), np.log(10.0), generator=g))
+    w = (w * mult.repeat_interleave(128, 0).repeat_interleave(128, 1)).bfloat16()
+    r = hip_per_block_quant(w.to(dev), block_m=128, block_n=128)
+    q_ref, s_ref = O.quant_block(w, 128, 128, threads=8)
+    assert r.dequant_scale.shape == (32, 56)
+    assert_same(r, q_ref, s_ref, "config3")
+
+
+# ---------------------------------------------------------------------------
+# per-channel
+# ---------------------------------------------------------------------------
+CHANNEL_CASES = [
+    ((33, 200), "bf16", -2, "e4m3"),        # register-resident rows
+    ((2, 40, 7168), "bf16", -2, "e4m3"),    # 14 chunk slots per lane
+    ((2, 16, 8200), "bf16", -2, "e4m3"),    # longer than 8192: generic two-pass row
+    ((50, 70), "f32", -2, "e4m3"),          # generic (n % 8 != 0)
+    ((3, 300, 264), "bf16", -1, "e4m3"),    # column strips
+    ((50, 70), "f32", -1, "e5m2"),          # generic columns
+    ((1, 4096, 512), "f16", -1, "e4m3"),    # tall column strips
+    ((64, 1024), "f32", -2, "e5m2"),        # fp32 rows
+]
+
+
+@pytest.mark.parametrize("shape,dtype,axis,fmt", CHANNEL_CASES)
+def test_channel_quant_matches_oracle(dev, shape, dtype, axis, fmt):
+    x = make_input(shape, dtype, seed=hash((shape, axis)) & 0xFFFF, scale=0.02, outliers=0.001)
+    print(f"channel {shape} {dtype} axis={axis} {fmt}", flush=True)
+    r = hip_per_channel_quant(x.to(dev), channel_axis=axis, fp8_dtype=FMT[fmt])
+    q_ref, s_ref = O.quant_channel(x, axis, fmt, threads=8)
+    assert r.dequant_scale.shape == s_ref.shape
+    assert_same(r, q_ref, s_ref, f"{shape} axis {axis}")
+
+
+def test_channel_one_pass_same_bytes(dev):
+    x = make_input((64, 4096), "bf16", seed=11).to(dev)
+    a = hip_per_channel_quant(x, channel_axis=-2, one_pass=True)
+    b = hip_per_channel_quant(x, channel_axis=-2)
+    assert a.meta["quant_strategy"] == "one_pass" and b.meta["quant_strategy"] == "two_pass"
+    assert torch.equal(a.tensor.view(torch.uint8), b.tensor.view(torch.uint8))
+    assert torch.equal(a.dequant_scale, b.dequant_scale)
+
+
+def test_config2_full_size(dev):
+    """bf16 weight [18432, 7168] N(0, 0.02), one scale per row."""
+    g = torch.Generator().manual_seed(0)
+    w = (torch.randn(18432, 7168, generator=g) * 0.02).bfloat16()
+    r = hip_per_channel_quant(w.to(dev), channel_axis=-2)
+    q_ref, s_ref = O.quant_channel(w, -2, threads=8)
+    assert r.dequant_scale.shape == (18432,)
+    assert_same(r, q_ref, s_ref, "config2")
+
+
+# ---------------------------------------------------------------------------
+# per-tensor
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("shape,dtype,fmt", [((3, 17, 33), "bf16", "e4m3"), ((64, 64), "f32", "e4m3"),
+                                             ((14, 2048, 512), "f32", "e5m2"), ((128, 256), "f16", "e4m3")])
+def test_tensor_quant_matches_oracle(dev, shape, dtype, fmt):
+    x = make_input(shape, dtype, seed=7, scale=3.0, outliers=0.001)
+    r = hip_per_tensor_quant(x.to(dev), fp8_dtype=FMT[fmt])
+    q_ref, ds, _ = O.quant_tensor(x, fmt)
+    assert r.dequant_scale.ndim == 0
+    assert_same(r, q_ref, np.float32(ds), f"tensor {shape}")
+
+
+def test_determinism(dev):
+    x = make_input((512, 7168), "bf16", seed=9).to(dev)
+    a = hip_per_block_quant(x, block_m=1, block_n=128)
+    b = hip_per_block_quant(x, block_m=1, block_n=128)
+    assert torch.equal(a.tensor.view(torch.uint8), b.tensor.view(torch.uint8))
+    assert torch.equal(a.dequant_scale, b.dequant_scale)
+
+
+def test_dequant_roundtrip(dev):
+    # reference fp8_quant_test.py:110-119: |x_hat - x| <= 0.1|x| + 0.05 amax
+    x = make_input((32, 2048), "f32", seed=10).to(dev)
+    for r in (hip_per_block_quant(x, block_m=1, block_n=128),
+              hip_per_channel_quant(x, channel_axis=-2),
+              hip_per_tensor_quant(x)):
+        xh = r.dequantize()
+        assert torch.allclose(xh, x, rtol=1e-1, atol=0.05 * x.abs().max().item())
