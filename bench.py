@@ -1,0 +1,336 @@
+"""Benchmark of the MI355X FP8 hot path (one GPU).
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-components] [--no-cpu-baseline]
+
+Prints ONE JSON line. The headline workload is BASELINE.json configs[1]:
+per-channel (one scale per row) bf16 -> fp8 e4m3 quantization of an
+[18432, 7168] weight. A step is one quantization of that tensor; K steps are
+captured back to back in a HIP graph over 4 rotating input/output sets
+(1.6 GB, far beyond the 256 MB MALL, so every step streams from HBM) and
+timed with HIP events on the stream the kernels run on. Inputs are resident
+in HBM before the timed region starts.
+
+``components`` reports the other BASELINE configs the same way (1x128 quant,
+128x128 quant, the block-scaled BMM of config 4 and the config-5 GEMM trio).
+``cpu_baseline`` times the CPU restatement of the same quantizer (oracle/,
+OpenMP over rows) on the host cores.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0        # MI355X HBM3E
+FP8_PEAK_TFLOPS = 5000.0     # MI355X dense fp8 MFMA (5.0 PFLOP/s)
+
+
+def parse():
+    p = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=50)
+    p.add_argument("--warmup", type=int, default=10)
+    p.add_argument("--no-components", action="store_true")
+    p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--components-only", default="", help="comma list of component names")
+    return p.parse_args()
+
+
+# ---------------------------------------------------------------------------
+# timing helpers
+# ---------------------------------------------------------------------------
+def graph_time(torch, launch, steps: int, warmup: int, reps: int = 3):
+    """Capture `steps` calls of launch(i) into one HIP graph and time replays.
+
+    Returns (ms per step over the best-of-reps replay, list of per-rep ms)."""
+    for i in range(warmup):
+        launch(i)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for i in range(steps):
+            launch(i)
+    g.replay()  # untimed replay: first-touch of the graph itself
+    torch.cuda.synchronize()
+    samples = []
+    for _ in range(reps):
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        start.record()
+        g.replay()
+        end.record()
+        torch.cuda.synchronize()
+        samples.append(start.elapsed_time(end) / steps)
+    return statistics.median(samples), samples
+
+
+# ---------------------------------------------------------------------------
+# inputs (CPU generator seeded 0, then copied to HBM)
+# ---------------------------------------------------------------------------
+def make_config1(torch):
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(4096, 7168, generator=g)
+    m = torch.rand(4096, 7168, generator=g) < 0.001
+    x[m] *= 50
+    return x.bfloat16()
+
+
+def make_config2(torch):
+    g = torch.Generator().manual_seed(0)
+    return (torch.randn(18432, 7168, generator=g) * 0.02).bfloat16()
+
+
+def make_config3(torch):
+    import math
+    g = torch.Generator().manual_seed(0)
+    w = torch.randn(4096, 7168, generator=g) * 0.02
+    mult = torch.exp(torch.empty(32, 56).uniform_(math.log(0.1), math.log(10.0), generator=g))
+    return (w * mult.repeat_interleave(128, 0).repeat_interleave(128, 1)).bfloat16()
+
+
+def rotate_sets(torch, x_cpu, nsets, dev):
+    """nsets distinct device copies of the input (first one exact, the others
+    perturbed in the last mantissa bit so no two sets share cache lines)."""
+    sets = []
+    for i in range(nsets):
+        x = x_cpu.to(dev)
+        if i:
+            x.view(torch.int16).bitwise_xor_(i & 1)
+        sets.append(x)
+    return sets
+
+
+# ---------------------------------------------------------------------------
+# quantizer workloads through the C ABI with preallocated outputs
+# ---------------------------------------------------------------------------
+def quant_channel_launcher(torch, L, xs, ys, ss):
+    def launch(i):
+        x, y, s = xs[i % len(xs)], ys[i % len(ys)], ss[i % len(ss)]
+        rc = L.lib().pcamd_quant_channel(
+            L.ptr(x), L.BF16, 1, x.shape[0], x.shape[1], 0, x.stride(0), 1,
+            L.ptr(y), L.E4M3FN, 0, y.stride(0), 1, L.ptr(s), 0, 1, -2, 448.0, 1e-12,
+            L.stream_of(x))
+        L.check(rc, "pcamd_quant_channel")
+    return launch
+
+
+def quant_block_launcher(torch, L, xs, ys, ss, bm, bn):
+    def launch(i):
+        x, y, s = xs[i % len(xs)], ys[i % len(ys)], ss[i % len(ss)]
+        rc = L.lib().pcamd_quant_block(
+            L.ptr(x), L.BF16, 1, x.shape[0], x.shape[1], 0, x.stride(0), 1,
+            L.ptr(y), L.E4M3FN, 0, y.stride(0), 1, L.ptr(s), 0, s.stride(0), 1,
+            bm, bn, 448.0, 1e-12, L.stream_of(x))
+        L.check(rc, "pcamd_quant_block")
+    return launch
+
+
+def bench_quant(torch, name, x_cpu, kind, steps, warmup, nsets, dev, bm=1, bn=128):
+    from practice_cuda_amd import _lib as L
+    m, n = x_cpu.shape
+    xs = rotate_sets(torch, x_cpu, nsets, dev)
+    ys = [torch.empty(m, n, dtype=torch.float8_e4m3fn, device=dev) for _ in range(nsets)]
+    if kind == "channel":
+        ss = [torch.empty(m, dtype=torch.float32, device=dev) for _ in range(nsets)]
+        launch = quant_channel_launcher(torch, L, xs, ys, ss)
+        scale_bytes = m * 4
+    else:
+        mb, nb = -(-m // bm), -(-n // bn)
+        ss = [torch.empty(mb, nb, dtype=torch.float32, device=dev) for _ in range(nsets)]
+        launch = quant_block_launcher(torch, L, xs, ys, ss, bm, bn)
+        scale_bytes = mb * nb * 4
+    ms, samples = graph_time(torch, launch, steps, warmup)
+    nbytes = m * n * 2 + m * n + scale_bytes
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    del xs, ys, ss
+    torch.cuda.empty_cache()
+    return {"name": name, "ms_per_step": ms, "samples_ms": samples, "bytes_per_step": nbytes,
+            "value": gbs, "unit": "GB/s", "frac_of_hbm_peak": gbs / HBM_PEAK_GBS}
+
+
+# ---------------------------------------------------------------------------
+# BMM workloads
+# ---------------------------------------------------------------------------
+def bench_config4(torch, steps, warmup, dev, nsets=4):
+    from practice_cuda_amd import _lib as L
+    from practice_cuda_amd.impls.hip_per_block import hip_per_block_quant
+    g = torch.Generator().manual_seed(0)
+    ah = torch.randn(128, 2048, 128, generator=g).bfloat16().to(dev)
+    bh = torch.randn(128, 128, 512, generator=g).bfloat16().to(dev)
+    qas, qbs, outs = [], [], []
+    for i in range(nsets):
+        qa = hip_per_block_quant(ah if i == 0 else ah * (1 + i / 64), block_m=1, block_n=128)
+        qb = hip_per_block_quant(bh, block_m=128, block_n=128)
+        qas.append(qa), qbs.append(qb)
+        outs.append(torch.empty(128, 2048, 512, dtype=torch.bfloat16, device=dev))
+
+    def launch(i):
+        qa, qb, c = qas[i % nsets], qbs[i % nsets], outs[i % nsets]
+        a, b, sa, sb = qa.tensor, qb.tensor, qa.dequant_scale, qb.dequant_scale
+        rc = L.lib().pcamd_bmm_scaled(
+            L.ptr(a), L.ptr(b), L.E4M3FN, 128, 2048, 512, 128, *a.stride(), *b.stride(),
+            L.ptr(c), L.BF16, *c.stride(), None, 0, 0, 0, 0,
+            L.ptr(sa), *sa.stride(), L.ptr(sb), *sb.stride(),
+            L.SCALE_BLOCK, 0, 1, 128, 128, L.ACT_NONE, L.stream_of(c))
+        L.check(rc, "pcamd_bmm_scaled")
+
+    ms, samples = graph_time(torch, launch, steps, warmup)
+    flops = 2 * 128 * 2048 * 512 * 128
+    nbytes = 128 * 2048 * 128 + 128 * 128 * 512 + 128 * 2048 * 512 * 2 + 128 * 2048 * 4 + 128 * 4 * 4
+    tflops = flops / (ms * 1e-3) / 1e12
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    attainable = min(FP8_PEAK_TFLOPS, HBM_PEAK_GBS * flops / nbytes / 1e3)
+    return {"name": "config4_block_bmm_b128_m2048_n512_k128", "ms_per_step": ms, "samples_ms": samples,
+            "value": tflops, "unit": "TFLOP/s", "frac_of_fp8_peak": tflops / FP8_PEAK_TFLOPS,
+            "hbm_GBps": gbs, "frac_of_hbm_peak": gbs / HBM_PEAK_GBS,
+            "frac_of_attainable_roofline": tflops / attainable, "bytes_per_step": nbytes,
+            "flops_per_step": flops}
+
+
+def bench_config5(torch, steps, warmup, dev):
+    """FP8 training-linear GEMM trio at M=8192 K=4096 N=14336: fwd X W^T
+    (a_k_b_k), dgrad dY W (a_k_b_n), wgrad dY^T X (a_m_b_n, 128x1 requant)."""
+    from practice_cuda_amd.impls.hip_per_block import hip_per_block_bmm, hip_per_block_quant
+    M, K, N = 8192, 4096, 14336
+    g = torch.Generator().manual_seed(0)
+    X = torch.randn(M, K, generator=g).bfloat16().to(dev)
+    W = (torch.randn(N, K, generator=g) * 0.02).bfloat16().to(dev)
+    dY = (torch.randn(M, N, generator=g) * 1e-3).bfloat16().to(dev)
+    qx = hip_per_block_quant(X[None], block_m=1, block_n=128)            # [1, M, K] 1x128
+    qw = hip_per_block_quant(W[None], block_m=128, block_n=128)          # [1, N, K] 128x128
+    qdy = hip_per_block_quant(dY[None], block_m=1, block_n=128)          # [1, M, N] 1x128
+    qdy_m = hip_per_block_quant(dY[None], block_m=128, block_n=1)        # [1, M, N] 128x1
+    qx_m = hip_per_block_quant(X[None], block_m=128, block_n=1)          # [1, M, K] 128x1
+    from practice_cuda_amd.registry import QuantResult
+
+    def tr(q: QuantResult, bm, bn):
+        # logical transpose of the last two dims (a strided view) with its scales
+        return QuantResult(q.tensor.transpose(-1, -2), q.dequant_scale.transpose(-1, -2), q.impl,
+                           "block", {"block_m": bn, "block_n": bm})
+
+    wt = tr(qw, 128, 128)         # B = W^T  [1, K, N], K-major     (fwd)
+    dyt = tr(qdy_m, 128, 1)       # A = dY^T [1, N, M], M-major     (wgrad), 1x128 over M
+    out_f = torch.empty(1, M, N, dtype=torch.bfloat16, device=dev)
+    out_d = torch.empty(1, M, K, dtype=torch.bfloat16, device=dev)
+    out_w = torch.empty(1, N, K, dtype=torch.bfloat16, device=dev)
+    gemms = {
+        "fwd_a_k_b_k": lambda i: hip_per_block_bmm(qx, wt, out=out_f),
+        "dgrad_a_k_b_n": lambda i: hip_per_block_bmm(qdy, qw, out=out_d),
+        "wgrad_a_m_b_n": lambda i: hip_per_block_bmm(dyt, qx_m, out=out_w),
+    }
+    flops = 2 * M * N * K
+    res = {}
+    for name, fn in gemms.items():
+        ms, samples = graph_time(torch, fn, steps, warmup)
+        t = flops / (ms * 1e-3) / 1e12
+        res[name] = {"ms": ms, "TFLOP/s": t, "frac_of_fp8_peak": t / FP8_PEAK_TFLOPS}
+    total_ms = sum(r["ms"] for r in res.values())
+    tflops = 3 * flops / (total_ms * 1e-3) / 1e12
+    return {"name": "config5_training_linear_m8192_k4096_n14336", "ms_per_step": total_ms,
+            "value": tflops, "unit": "TFLOP/s", "frac_of_fp8_peak": tflops / FP8_PEAK_TFLOPS,
+            "gemms": res, "flops_per_step": 3 * flops}
+
+
+# ---------------------------------------------------------------------------
+# CPU baseline: the oracle's OpenMP restatement of the same quantizer
+# ---------------------------------------------------------------------------
+def cpu_baseline(torch, x_cpu):
+    from oracle import oracle as O
+    threads = min(os.cpu_count() or 1, 16)
+    sample = x_cpu.contiguous()                 # the full workload tensor
+    O.quant_channel(sample[:64], -2, threads=threads)   # warm (page-in, thread pool)
+    times = []
+    for _ in range(5):
+        t0 = time.perf_counter()
+        O.quant_channel(sample, -2, threads=threads)
+        times.append(time.perf_counter() - t0)
+    t = statistics.median(times)
+    m, n = sample.shape
+    nbytes = m * n * 3 + m * 4
+    return {"value": nbytes / t / 1e9, "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"bf16 [{m},{n}] (the full workload tensor), "
+                      f"median of 5 runs of oracle/fp8_oracle.c per-channel quant, "
+                      f"{threads} OpenMP threads, {t * 1e3:.1f} ms/run"}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on exactly one GPU; --gpus must be 1 "
+                          "(multi-GPU sharding is documented in DESIGN.md, not launched)"}))
+        sys.exit(2)
+    import torch
+
+    from practice_cuda_amd import _lib
+    _lib.lib()
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+
+    x2 = make_config2(torch)
+    head = bench_quant(torch, "config2_per_channel_quant_18432x7168", x2, "channel",
+                       args.steps, args.warmup, 4, dev)
+    ms = head["ms_per_step"]
+    line = {
+        "metric": "quant GB/s and FP8 BMM TFLOP/s at 1 MI355X, % of HBM / fp8-MFMA peak",
+        "value": round(head["value"], 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16->fp8e4m3 (fp32 math)",
+        "data": "synthetic (BASELINE configs, CPU generator seed 0)",
+        "config": {"workload": "BASELINE configs[1]: per-channel fp8 quant, bf16 weight [18432,7168] "
+                               "-> e4m3 + fp32 row scales [18432], channel_axis=-2",
+                   "shape": [18432, 7168], "rotating_buffer_sets": 4, "timing": "HIP graph of K launches"},
+        "roofline": {"bound": "hbm", "achieved": round(head["value"], 2), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(head["value"] / HBM_PEAK_GBS, 4),
+                     "traffic": None, "kernel": "quant_rows_kernel<bf16,e4m3,64,whole_row>",
+                     "bytes_per_launch": head["bytes_per_step"]},
+    }
+    traffic_file = os.path.join(ROOT, "profiles", "traffic.json")
+    if os.path.exists(traffic_file):
+        with open(traffic_file) as fh:
+            t = json.load(fh).get("config2_per_channel_quant")
+        if t:
+            line["roofline"]["traffic"] = t["hbm_bytes_per_launch"]
+
+    if not args.no_components:
+        only = set(filter(None, args.components_only.split(",")))
+        comps = []
+        try:
+            if not only or "config1" in only:
+                comps.append(bench_quant(torch, "config1_1x128_quant_4096x7168", make_config1(torch),
+                                         "block", args.steps, args.warmup, 8, dev, 1, 128))
+            if not only or "config3" in only:
+                comps.append(bench_quant(torch, "config3_128x128_quant_4096x7168", make_config3(torch),
+                                         "block", args.steps, args.warmup, 8, dev, 128, 128))
+            if not only or "config4" in only:
+                comps.append(bench_config4(torch, args.steps, args.warmup, dev))
+            if not only or "config5" in only:
+                comps.append(bench_config5(torch, max(2, args.steps // 10), 2, dev))
+        except Exception as exc:  # a component failure must not hide the headline
+            comps.append({"error": repr(exc)})
+        for c in comps:
+            for k, v in list(c.items()):
+                if isinstance(v, float):
+                    c[k] = round(v, 5)
+        line["components"] = comps
+
+    if not args.no_cpu_baseline:
+        line["cpu_baseline"] = cpu_baseline(torch, x2)
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()

@@ -33,8 +33,10 @@
 
 #include <algorithm>
 #include <cstdint>
+#include <cstdlib>
 
 #include "abi_util.h"
+#include "bmm_fast.h"
 #include "fp8_common.h"
 
 namespace pcamd {
@@ -486,6 +488,44 @@ extern "C" int pcamd_bmm_scaled(const void* a, const void* b, int ab_dtype, int6
   args.vec_a = al16(a) && (sab % 16 == 0) && (a_k ? sam % 16 == 0 : sak % 16 == 0);
   args.vec_b = al16(b) && (sbb % 16 == 0) && (b_k ? sbn % 16 == 0 : sbk % 16 == 0);
   hipStream_t st = static_cast<hipStream_t>(stream);
+
+  // tuned path: K a multiple of 128, 16-byte aligned operands and rows,
+  // power-of-two block sizes, 32-bit addressable batch slices
+  {
+    const int64_t TM = bmm_fast_tile_m(), TN = bmm_fast_tile_n();
+    const int64_t tm = (m + TM - 1) / TM, tn = (n + TN - 1) / TN;
+    const int64_t lda = a_k ? sam : sak, ldb = b_k ? sbn : sbk;
+    // largest byte offset a workgroup can form (rows padded to the tile)
+    const int64_t a_max = a_k ? (tm * TM) * lda + k : (k - 1) * lda + tm * TM;
+    const int64_t b_max = b_k ? (tn * TN) * ldb + k : (k - 1) * ldb + tn * TN;
+    const bool block_ok = scale_mode != PCAMD_SCALE_BLOCK ||
+                          (args.qbm_shift >= 0 && args.qbn_shift >= 0);
+    const bool fast = k > 0 && k % 128 == 0 && args.vec_a && args.vec_b && lda % 16 == 0 && ldb % 16 == 0 &&
+                      a_max < (int64_t{1} << 32) - 64 && b_max < (int64_t{1} << 32) - 64 &&
+                      m < INT32_MAX && n < INT32_MAX && k < INT32_MAX && tm * tn * batch < INT32_MAX &&
+                      block_ok && getenv("PCAMD_BMM_GENERIC") == nullptr;
+    if (fast) {
+      FastArgs f{};
+      f.a = args.a; f.b = args.b; f.c = c; f.bias = bias; f.sa = sa; f.sb = sb;
+      f.m = static_cast<int32_t>(m); f.n = static_cast<int32_t>(n); f.k = static_cast<int32_t>(k);
+      f.sab = sab; f.sbb = sbb;
+      f.lda = static_cast<uint32_t>(lda); f.ldb = static_cast<uint32_t>(ldb);
+      f.a_extent = static_cast<uint32_t>(a_k ? (m - 1) * sam + k : (k - 1) * sak + m);
+      f.b_extent = static_cast<uint32_t>(b_k ? (n - 1) * sbn + k : (k - 1) * sbk + n);
+      f.scb = scb; f.scm = scm; f.scn = scn;
+      f.sbiasb = sbiasb; f.sbiasm = sbiasm; f.sbiasn = sbiasn;
+      f.ssab = ssab; f.ssa1 = ssa1; f.ssa2 = ssa2; f.ssbb = ssbb; f.ssb1 = ssb1; f.ssb2 = ssb2;
+      f.qbk = static_cast<int32_t>(args.qbk); f.qbm_shift = args.qbm_shift; f.qbn_shift = args.qbn_shift;
+      f.tiles_m = static_cast<int32_t>(tm); f.tiles_n = static_cast<int32_t>(tn);
+      f.tiles_per_batch = static_cast<int32_t>(tm * tn);
+      f.total_tiles = static_cast<int32_t>(tm * tn * batch);
+      f.c_dtype = c_dtype; f.bias_dtype = bias_dtype; f.act = activation; f.scales_are_quant = scales_are_quant;
+      const int fmode = scale_mode == PCAMD_SCALE_BLOCK ? 0 : scale_mode == PCAMD_SCALE_CHANNEL ? 1 : 2;
+      const bool sb_col = scale_mode == PCAMD_SCALE_BLOCK && args.qbn < 16;
+      const bool qb1 = scale_mode == PCAMD_SCALE_BLOCK && args.qbk == 128;
+      return bmm_fast_launch(f, ab_dtype, a_k, b_k, fmode, sb_col, qb1, st);
+    }
+  }
   if (ab_dtype == kE5M2) return bmm::launch_layout<kE5M2>(args, a_k, b_k, mode, st);
   return bmm::launch_layout<kE4M3>(args, a_k, b_k, mode, st);
 }

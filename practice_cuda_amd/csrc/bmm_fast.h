@@ -1,0 +1,37 @@
+// bmm_fast.h - arguments and launcher of the tuned FP8 BMM path (bmm_fast.hip).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace pcamd {
+
+struct FastArgs {
+  const uint8_t* a;
+  const uint8_t* b;
+  void* c;
+  const void* bias;
+  const float* sa;
+  const float* sb;
+  int32_t m, n, k;
+  int64_t sab, sbb;            // batch strides of a / b (bytes)
+  uint32_t lda, ldb;           // stride between the rows the kernel walks (bytes):
+                               //   A k-major: m rows; A m-major: k rows
+                               //   B k-major: n rows; B n-major: k rows
+  uint32_t a_extent, b_extent; // bytes addressable in one batch slice (buffer bounds)
+  int64_t scb, scm, scn;
+  int64_t sbiasb, sbiasm, sbiasn;
+  int64_t ssab, ssa1, ssa2, ssbb, ssb1, ssb2;
+  int32_t qbk, qbm_shift, qbn_shift;
+  int32_t tiles_m, tiles_n, tiles_per_batch, total_tiles;
+  int32_t c_dtype, bias_dtype, act, scales_are_quant;
+};
+
+// mode: 0 block, 1 channel, 2 tensor
+int bmm_fast_launch(const FastArgs& a, int ab_dtype, bool a_k, bool b_k, int mode, bool sb_col, bool qb1,
+                    hipStream_t st);
+int bmm_fast_tile_m();
+int bmm_fast_tile_n();
+
+}  // namespace pcamd
