@@ -39,6 +39,9 @@ def parse():
     p.add_argument("--no-components", action="store_true")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--components-only", default="", help="comma list of component names")
+    p.add_argument("--pmc-probe", action="store_true",
+                   help="eager launches for rocprofv3 --pmc passes: 3 plain bf16 copies of "
+                        "256 MiB (calibration) then 3 config-2 quantizations")
     return p.parse_args()
 
 
@@ -260,6 +263,28 @@ def cpu_baseline(torch, x_cpu):
                       f"{threads} OpenMP threads, {t * 1e3:.1f} ms/run"}
 
 
+def pmc_probe(torch, dev):
+    """Known-size copy (calibration) and the headline kernel, launched eagerly
+    so every dispatch carries its own counters."""
+    from practice_cuda_amd import _lib as L
+    src = torch.ones(1 << 27, dtype=torch.bfloat16, device=dev)  # 256 MiB
+    dst = torch.empty_like(src)
+    x2 = make_config2(torch)
+    xs = rotate_sets(torch, x2, 3, dev)
+    ys = [torch.empty(x2.shape, dtype=torch.float8_e4m3fn, device=dev) for _ in range(3)]
+    ss = [torch.empty(x2.shape[0], dtype=torch.float32, device=dev) for _ in range(3)]
+    launch = quant_channel_launcher(torch, L, xs, ys, ss)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    for i in range(3):
+        launch(i)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_bytes_read": src.numel() * 2, "copy_bytes_written": dst.numel() * 2,
+                      "quant_bytes_read": x2.numel() * 2, "quant_bytes_written": x2.numel() + x2.shape[0] * 4}))
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -272,6 +297,10 @@ def main():
     _lib.lib()
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+
+    if args.pmc_probe:
+        pmc_probe(torch, dev)
+        return
 
     x2 = make_config2(torch)
     head = bench_quant(torch, "config2_per_channel_quant_18432x7168", x2, "channel",
@@ -295,7 +324,7 @@ def main():
                    "shape": [18432, 7168], "rotating_buffer_sets": 4, "timing": "HIP graph of K launches"},
         "roofline": {"bound": "hbm", "achieved": round(head["value"], 2), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(head["value"] / HBM_PEAK_GBS, 4),
-                     "traffic": None, "kernel": "quant_rows_kernel<bf16,e4m3,64,whole_row>",
+                     "traffic": None, "kernel": "quant_waverow_kernel<bf16,e4m3,16,nt>",
                      "bytes_per_launch": head["bytes_per_step"]},
     }
     traffic_file = os.path.join(ROOT, "profiles", "traffic.json")

@@ -1,14 +1,17 @@
 // quant.hip - gfx950 FP8 quantizers behind the C ABI (include/pcamd_fp8.h).
 //
 // Kernels (all HBM-bound; each element is read once from HBM):
-//   quant_rows_kernel   row-contiguous input; every lane owns an 8-element
-//                       chunk (one 128-bit load for bf16/fp16). Groups of
-//                       LPG lanes share a scale (per-block 1 x 8*LPG), or the
-//                       whole row held in registers shares one (per-channel,
-//                       channel_axis = -2). Amax via DPP inside the wave.
+//   quant_groups_kernel row-contiguous 1 x G groups: every lane owns 8-element
+//                       chunks (one 128-bit load for bf16/fp16), groups of
+//                       G/8 lanes reduce their amax with DPP; persistent
+//                       waves with the next unit prefetched in registers.
+//   quant_rowblock_kernel  per-channel along rows (channel_axis = -2): a
+//                       workgroup holds a row (up to 16384 elements), DPP +
+//                       one LDS max; persistent, next row prefetched.
 //   quant_tile_kernel   one workgroup per block_m x block_n block held in
 //                       registers (e.g. 128 x 128 = 8 chunks per thread);
-//                       wave DPP max, then an LDS max across the 4 waves.
+//                       wave DPP max, then an LDS max across the 4 waves;
+//                       persistent, next block prefetched.
 //   quant_cols_kernel   row-contiguous input with column groups (block_n = 1,
 //                       16 <= block_m <= 256, held in registers) or whole
 //                       columns (channel_axis = -1, two passes over the strip).
@@ -24,6 +27,7 @@
 
 #include <algorithm>
 #include <cstdint>
+#include <cstdlib>
 
 #include "abi_util.h"
 #include "fp8_common.h"
@@ -34,84 +38,175 @@ constexpr int kThreads = 256;
 constexpr int kMaxSlots = 16;  // chunk slots held in registers per lane
 
 // ===========================================================================
-// row-contiguous kernel
+// row-contiguous kernels (persistent waves, next unit prefetched in registers)
 // ===========================================================================
 struct RowArgs {
   const char* x;
   uint8_t* y;
   float* scale;
-  int64_t m;      // rows per batch
-  int64_t sxb, sxm;  // input strides (elements)
-  int64_t syb, sym;  // output strides (bytes == elements)
+  uint32_t m;       // rows per batch
+  int64_t sxb, sxm; // input strides (elements)
+  int64_t syb, sym; // output strides (bytes == elements)
   int64_t ssb, ssm, ssn;  // scale strides (elements)
-  int64_t units;  // rows * segs
-  int32_t chunks; // 8-element chunks per row
-  int32_t cpl;    // chunk slots per lane per segment (<= kMaxSlots)
-  int32_t segs;   // segments per row
+  uint32_t units;   // rows * segs
+  int32_t chunks;   // 8-element chunks per row
+  int32_t cpl;      // chunk slots per lane (wave-per-row kernel)
+  uint32_t segs;    // segments per row (group kernel)
   float fp8_max, eps;
 };
 
-template <int DT, int FMT, int LPG, bool WHOLE_ROW>
-__global__ __launch_bounds__(kThreads) void quant_rows_kernel(RowArgs a) {
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+
+template <int DT, bool NTS>
+PCAMD_DEV void store8(uint8_t* p, uint2 v) {
+  if constexpr (NTS) {
+    u32x2 w = {v.x, v.y};
+    __builtin_nontemporal_store(w, reinterpret_cast<u32x2*>(p));
+  } else {
+    *reinterpret_cast<uint2*>(p) = v;
+  }
+}
+
+// 1 x (8 * LPG) groups along a row. A unit is CPL * 64 consecutive chunks of
+// one row; each wave walks units with a stride of the whole grid and has the
+// next unit's loads in flight while it reduces, scales and stores the current.
+template <int DT, int FMT, int LPG, int CPL, bool NTS>
+__global__ __launch_bounds__(kThreads) void quant_groups_kernel(RowArgs a) {
   constexpr int EB = elem_bytes<DT>();
   const int lane = threadIdx.x & 63;
-  const int64_t nwaves = static_cast<int64_t>(gridDim.x) * (kThreads / 64);
-  for (int64_t u = static_cast<int64_t>(blockIdx.x) * (kThreads / 64) + (threadIdx.x >> 6);
-       u < a.units; u += nwaves) {
-    const int64_t row = u / a.segs;
-    const int seg = static_cast<int>(u - row * a.segs);
-    const int64_t b = row / a.m;
-    const int64_t mi = row - b * a.m;
-    const char* xrow = a.x + (b * a.sxb + mi * a.sxm) * EB;
-    uint8_t* yrow = a.y + b * a.syb + mi * a.sym;
-    const int chunk0 = seg * a.cpl * 64 + lane;
+  const uint32_t nwaves = gridDim.x * (kThreads / 64);
+  uint32_t u = blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6);
 
-    Chunk<DT> raw[kMaxSlots];
+  auto locate = [&](uint32_t uu, uint32_t& b, uint32_t& mi, int& chunk0) {
+    const uint32_t row = uu / a.segs;
+    const uint32_t seg = uu - row * a.segs;
+    b = row / a.m;
+    mi = row - b * a.m;
+    chunk0 = static_cast<int>(seg) * CPL * 64 + lane;
+  };
+  auto load_unit = [&](uint32_t uu, Chunk<DT> (&buf)[CPL]) {
+    uint32_t b, mi;
+    int chunk0;
+    locate(uu, b, mi, chunk0);
+    const char* xrow = a.x + (int64_t(b) * a.sxb + int64_t(mi) * a.sxm) * EB;
 #pragma unroll
-    for (int c = 0; c < kMaxSlots; ++c) {
-      if (c < a.cpl) {
-        const int ch = chunk0 + c * 64;
-        if (ch < a.chunks) load_chunk<DT>(raw[c], xrow + static_cast<int64_t>(ch) * 8 * EB);
-        else zero_chunk<DT>(raw[c]);
+    for (int c = 0; c < CPL; ++c) {
+      const int ch = chunk0 + c * 64;
+      if (ch < a.chunks) load_chunk<DT>(buf[c], xrow + int64_t(ch) * 8 * EB);
+      else zero_chunk<DT>(buf[c]);
+    }
+  };
+
+  Chunk<DT> cur[CPL], nxt[CPL];
+  if (u < a.units) load_unit(u, cur);
+  for (; u < a.units; u += nwaves) {
+    const uint32_t un = u + nwaves;
+    if (un < a.units) load_unit(un, nxt);
+    uint32_t b, mi;
+    int chunk0;
+    locate(u, b, mi, chunk0);
+    uint8_t* yrow = a.y + int64_t(b) * a.syb + int64_t(mi) * a.sym;
+    float* srow = a.scale + int64_t(b) * a.ssb + int64_t(mi) * a.ssm;
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) {
+      const int ch = chunk0 + c * 64;
+      const float amax = group_max<LPG>(chunk_amax<DT>(cur[c]));
+      const Scales s = block_scales(amax, a.fp8_max, a.eps);
+      if (ch < a.chunks) {
+        if ((lane & (LPG - 1)) == 0) srow[int64_t(ch / LPG) * a.ssn] = s.ds;
+        store8<DT, NTS>(yrow + int64_t(ch) * 8, quant_chunk<DT, FMT>(cur[c], s.qs, a.fp8_max));
       }
     }
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) cur[c] = nxt[c];
+  }
+}
 
-    if constexpr (WHOLE_ROW) {
-      // one segment per row (host guarantees segs == 1): one scale per row
-      float amax = 0.0f;
+// Per-channel along the row, one wave per row: the row (up to 64 * MAXC
+// chunks) is held in registers and read from HBM once. Non-persistent:
+// enough waves are resident that their load, reduce and store phases overlap.
+template <int DT, int FMT, int MAXC, bool NTS>
+__global__ __launch_bounds__(kThreads) void quant_waverow_kernel(RowArgs a) {
+  constexpr int EB = elem_bytes<DT>();
+  const int lane = threadIdx.x & 63;
+  const uint32_t row = blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6);
+  if (row >= a.units) return;  // whole waves exit together
+  const uint32_t b = row / a.m, mi = row - b * a.m;
+  const char* xrow = a.x + (int64_t(b) * a.sxb + int64_t(mi) * a.sxm) * EB;
+  Chunk<DT> raw[MAXC];
 #pragma unroll
-      for (int c = 0; c < kMaxSlots; ++c)
-        if (c < a.cpl) amax = fmaxf(amax, chunk_amax<DT>(raw[c]));
-      amax = group_max<64>(amax);
-      const Scales s = channel_scales(amax, a.fp8_max, a.eps);
-      if (lane == 0) a.scale[b * a.ssb + mi * a.ssm] = s.ds;
+  for (int c = 0; c < MAXC; ++c) {
+    const int ch = lane + c * 64;
+    if (c < a.cpl && ch < a.chunks) load_chunk<DT>(raw[c], xrow + int64_t(ch) * 8 * EB);
+    else zero_chunk<DT>(raw[c]);
+  }
+  float amax = 0.0f;
 #pragma unroll
-      for (int c = 0; c < kMaxSlots; ++c) {
-        const int ch = chunk0 + c * 64;
-        if (c < a.cpl && ch < a.chunks)
-          *reinterpret_cast<uint2*>(yrow + static_cast<int64_t>(ch) * 8) =
-              quant_chunk<DT, FMT>(raw[c], s.qs, a.fp8_max);
-      }
-    } else {
+  for (int c = 0; c < MAXC; ++c) amax = fmaxf(amax, chunk_amax<DT>(raw[c]));
+  amax = group_max<64>(amax);
+  const Scales s = channel_scales(amax, a.fp8_max, a.eps);
+  if (lane == 0) a.scale[int64_t(b) * a.ssb + int64_t(mi) * a.ssm] = s.ds;
+  uint8_t* yrow = a.y + int64_t(b) * a.syb + int64_t(mi) * a.sym;
 #pragma unroll
-      for (int c = 0; c < kMaxSlots; ++c) {
-        if (c < a.cpl) {
-          const int ch = chunk0 + c * 64;
-          const float amax = group_max<LPG>(chunk_amax<DT>(raw[c]));
-          const Scales s = block_scales(amax, a.fp8_max, a.eps);
-          if (ch < a.chunks) {
-            if ((lane & (LPG - 1)) == 0) a.scale[b * a.ssb + mi * a.ssm + (ch / LPG) * a.ssn] = s.ds;
-            *reinterpret_cast<uint2*>(yrow + static_cast<int64_t>(ch) * 8) =
-                quant_chunk<DT, FMT>(raw[c], s.qs, a.fp8_max);
-          }
-        }
-      }
+  for (int c = 0; c < MAXC; ++c) {
+    const int ch = lane + c * 64;
+    if (c < a.cpl && ch < a.chunks)
+      store8<DT, NTS>(yrow + int64_t(ch) * 8, quant_chunk<DT, FMT>(raw[c], s.qs, a.fp8_max));
+  }
+}
+
+// Per-channel along the row: one workgroup per row step (persistent over
+// rows), thread t owning chunks t, t + 256, ... (CPT of them, 256 * CPT >=
+// chunks). Wave DPP max, then one LDS exchange; the next row of the
+// workgroup is loaded while the current one is reduced and written.
+template <int DT, int FMT, int CPT, bool NTS>
+__global__ __launch_bounds__(kThreads) void quant_rowblock_kernel(RowArgs a) {
+  constexpr int EB = elem_bytes<DT>();
+  __shared__ float red[2][kThreads / 64];
+  const int t = threadIdx.x;
+  const uint32_t rows = a.units;
+
+  auto load_row = [&](uint32_t r, Chunk<DT> (&buf)[CPT]) {
+    const uint32_t b = r / a.m, mi = r - b * a.m;
+    const char* xrow = a.x + (int64_t(b) * a.sxb + int64_t(mi) * a.sxm) * EB;
+#pragma unroll
+    for (int c = 0; c < CPT; ++c) {
+      const int ch = t + c * kThreads;
+      if (ch < a.chunks) load_chunk<DT>(buf[c], xrow + int64_t(ch) * 8 * EB);
+      else zero_chunk<DT>(buf[c]);
     }
+  };
+
+  Chunk<DT> cur[CPT], nxt[CPT];
+  uint32_t row = blockIdx.x;
+  if (row < rows) load_row(row, cur);
+  for (int it = 0; row < rows; row += gridDim.x, ++it) {
+    if (row + gridDim.x < rows) load_row(row + gridDim.x, nxt);
+    float amax = 0.0f;
+#pragma unroll
+    for (int c = 0; c < CPT; ++c) amax = fmaxf(amax, chunk_amax<DT>(cur[c]));
+    amax = group_max<64>(amax);
+    float* rd = red[it & 1];  // alternating slots: one barrier per row
+    if ((t & 63) == 0) rd[t >> 6] = amax;
+    __syncthreads();
+    amax = fmaxf(fmaxf(rd[0], rd[1]), fmaxf(rd[2], rd[3]));
+    const Scales s = channel_scales(amax, a.fp8_max, a.eps);
+    const uint32_t b = row / a.m, mi = row - b * a.m;
+    if (t == 0) a.scale[int64_t(b) * a.ssb + int64_t(mi) * a.ssm] = s.ds;
+    uint8_t* yrow = a.y + int64_t(b) * a.syb + int64_t(mi) * a.sym;
+#pragma unroll
+    for (int c = 0; c < CPT; ++c) {
+      const int ch = t + c * kThreads;
+      if (ch < a.chunks) store8<DT, NTS>(yrow + int64_t(ch) * 8, quant_chunk<DT, FMT>(cur[c], s.qs, a.fp8_max));
+    }
+#pragma unroll
+    for (int c = 0; c < CPT; ++c) cur[c] = nxt[c];
   }
 }
 
 // ===========================================================================
-// tile kernel: one workgroup per block_m x block_n block
+// tile kernel: one block_m x block_n block per workgroup step (persistent,
+// the next block prefetched in registers)
 // ===========================================================================
 struct TileArgs {
   const char* x;
@@ -119,60 +214,69 @@ struct TileArgs {
   float* scale;
   int64_t m, n;
   int64_t sxb, sxm, syb, sym, ssb, ssm, ssn;
-  int64_t mb, nb;    // blocks along m, n
-  int64_t blocks;    // batch * mb * nb
+  uint32_t mb, nb;   // blocks along m, n
+  uint32_t blocks;   // batch * mb * nb
   int32_t block_m;
-  int32_t cpt;       // chunks per thread = block_m * LPR / 256
+  int32_t cpt;       // chunks per thread = block_m * lpr / 256
+  int32_t lpr, lpr_shift;  // lanes per block row (block_n / 8) and its log2
   float fp8_max, eps;
 };
 
-template <int DT, int FMT, int LPR>
+template <int DT, int FMT, int CPT, bool NTS>
 __global__ __launch_bounds__(kThreads) void quant_tile_kernel(TileArgs a) {
   constexpr int EB = elem_bytes<DT>();
-  constexpr int RPP = kThreads / LPR;  // rows per pass
-  __shared__ float red[kThreads / 64];
+  __shared__ float red[2][kThreads / 64];
   const int t = threadIdx.x;
-  const int rp = t / LPR, lr = t % LPR;
-  for (int64_t blk = blockIdx.x; blk < a.blocks; blk += gridDim.x) {
-    const int64_t b = blk / (a.mb * a.nb);
-    const int64_t rem = blk - b * a.mb * a.nb;
-    const int64_t pm = rem / a.nb, pn = rem - pm * a.nb;
-    const int64_t r0 = pm * a.block_m;
-    const int64_t col = pn * (LPR * 8) + lr * 8;
-    const char* xb = a.x + (b * a.sxb) * EB;
-    uint8_t* yb = a.y + b * a.syb;
+  const int lr = t & (a.lpr - 1), rp = t >> a.lpr_shift;  // lane in row, row in pass
+  const int rpp = kThreads >> a.lpr_shift;                 // rows per pass
 
-    Chunk<DT> raw[kMaxSlots];
+  auto locate = [&](uint32_t blk, uint32_t& b, uint32_t& pm, uint32_t& pn) {
+    b = blk / (a.mb * a.nb);
+    const uint32_t rem = blk - b * a.mb * a.nb;
+    pm = rem / a.nb;
+    pn = rem - pm * a.nb;
+  };
+  auto load_block = [&](uint32_t blk, Chunk<DT> (&buf)[CPT]) {
+    uint32_t b, pm, pn;
+    locate(blk, b, pm, pn);
+    const int64_t r0 = int64_t(pm) * a.block_m;
+    const int64_t col = int64_t(pn) * (a.lpr * 8) + lr * 8;
+    const char* xb = a.x + int64_t(b) * a.sxb * EB;
+#pragma unroll
+    for (int p = 0; p < CPT; ++p) {
+      const int64_t r = r0 + p * rpp + rp;
+      if (r < a.m && col < a.n) load_chunk<DT>(buf[p], xb + (r * a.sxm + col) * EB);
+      else zero_chunk<DT>(buf[p]);
+    }
+  };
+
+  Chunk<DT> cur[CPT], nxt[CPT];
+  uint32_t blk = blockIdx.x;
+  if (blk < a.blocks) load_block(blk, cur);
+  for (int it = 0; blk < a.blocks; blk += gridDim.x, ++it) {
+    if (blk + gridDim.x < a.blocks) load_block(blk + gridDim.x, nxt);
+    uint32_t b, pm, pn;
+    locate(blk, b, pm, pn);
     float amax = 0.0f;
 #pragma unroll
-    for (int p = 0; p < kMaxSlots; ++p) {
-      if (p < a.cpt) {
-        const int64_t r = r0 + p * RPP + rp;
-        if (r < a.m && col < a.n) {
-          load_chunk<DT>(raw[p], xb + (r * a.sxm + col) * EB);
-        } else {
-          zero_chunk<DT>(raw[p]);
-        }
-      }
-    }
-#pragma unroll
-    for (int p = 0; p < kMaxSlots; ++p)
-      if (p < a.cpt) amax = fmaxf(amax, chunk_amax<DT>(raw[p]));
+    for (int p = 0; p < CPT; ++p) amax = fmaxf(amax, chunk_amax<DT>(cur[p]));
     amax = group_max<64>(amax);
-    if ((t & 63) == 0) red[t >> 6] = amax;
+    float* rd = red[it & 1];  // alternating slots: one barrier per block
+    if ((t & 63) == 0) rd[t >> 6] = amax;
     __syncthreads();
-    amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-    __syncthreads();  // red[] is reused by the next block of this workgroup
+    amax = fmaxf(fmaxf(rd[0], rd[1]), fmaxf(rd[2], rd[3]));
     const Scales s = block_scales(amax, a.fp8_max, a.eps);
-    if (t == 0) a.scale[b * a.ssb + pm * a.ssm + pn * a.ssn] = s.ds;
+    if (t == 0) a.scale[int64_t(b) * a.ssb + int64_t(pm) * a.ssm + int64_t(pn) * a.ssn] = s.ds;
+    const int64_t r0 = int64_t(pm) * a.block_m;
+    const int64_t col = int64_t(pn) * (a.lpr * 8) + lr * 8;
+    uint8_t* yb = a.y + int64_t(b) * a.syb;
 #pragma unroll
-    for (int p = 0; p < kMaxSlots; ++p) {
-      if (p < a.cpt) {
-        const int64_t r = r0 + p * RPP + rp;
-        if (r < a.m && col < a.n)
-          *reinterpret_cast<uint2*>(yb + r * a.sym + col) = quant_chunk<DT, FMT>(raw[p], s.qs, a.fp8_max);
-      }
+    for (int p = 0; p < CPT; ++p) {
+      const int64_t r = r0 + p * rpp + rp;
+      if (r < a.m && col < a.n) store8<DT, NTS>(yb + r * a.sym + col, quant_chunk<DT, FMT>(cur[p], s.qs, a.fp8_max));
     }
+#pragma unroll
+    for (int p = 0; p < CPT; ++p) cur[p] = nxt[p];
   }
 }
 
@@ -483,42 +587,126 @@ int dispatch_dt_fmt(int dt, int fmt, Args&&... args) {
   return Launch<kF32, kE5M2>::run(args...);
 }
 
+// Workgroups that fit the device at once for `kern` (occupancy x CUs),
+// queried once per kernel instantiation.
+template <typename K>
+int resident_wgs(K kern) {
+  static int cached = 0;  // benign race: every thread computes the same value
+  if (!cached) {
+    int dev = 0, cus = 0, per_cu = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+      cus = 256;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void*>(kern), kThreads, 0) !=
+            hipSuccess || per_cu <= 0)
+      per_cu = 2;
+    cached = cus * per_cu;
+  }
+  return cached;
+}
+
+// persistent grid: as many workgroups as fit, with the work spread evenly
+inline int balanced_grid(int64_t work_wgs, int resident) {
+  if (work_wgs <= resident) return static_cast<int>(std::max<int64_t>(work_wgs, 1));
+  const int64_t rounds = (work_wgs + resident - 1) / resident;
+  return static_cast<int>((work_wgs + rounds - 1) / rounds);
+}
+
+// Quantized outputs are written once and not re-read by this kernel:
+// non-temporal stores measured 3-6% faster on MI355X. PCAMD_QUANT_NT=0
+// selects ordinary stores.
+inline bool nt_stores() {
+  static const int v = [] {
+    const char* e = getenv("PCAMD_QUANT_NT");
+    return e && e[0] == '0' ? 0 : 1;
+  }();
+  return v != 0;
+}
+
 template <int DT, int FMT>
-struct LaunchRows {
-  static int run(const RowArgs& a, int lpg, bool whole_row, hipStream_t st) {
-    const int grid = grid_for(a.units, kThreads / 64);
-    if (whole_row) {
-      quant_rows_kernel<DT, FMT, 64, true><<<grid, kThreads, 0, st>>>(a);
-    } else {
-      switch (lpg) {
-        case 1: quant_rows_kernel<DT, FMT, 1, false><<<grid, kThreads, 0, st>>>(a); break;
-        case 2: quant_rows_kernel<DT, FMT, 2, false><<<grid, kThreads, 0, st>>>(a); break;
-        case 4: quant_rows_kernel<DT, FMT, 4, false><<<grid, kThreads, 0, st>>>(a); break;
-        case 8: quant_rows_kernel<DT, FMT, 8, false><<<grid, kThreads, 0, st>>>(a); break;
-        case 16: quant_rows_kernel<DT, FMT, 16, false><<<grid, kThreads, 0, st>>>(a); break;
-        case 32: quant_rows_kernel<DT, FMT, 32, false><<<grid, kThreads, 0, st>>>(a); break;
-        case 64: quant_rows_kernel<DT, FMT, 64, false><<<grid, kThreads, 0, st>>>(a); break;
-        default: return set_error(PCAMD_ERR_UNSUPPORTED, "row kernel: unsupported lanes per group %d", lpg);
-      }
+struct LaunchGroups {
+  template <int LPG, int CPL, bool NTS>
+  static int go(const RowArgs& a, hipStream_t st) {
+    auto kern = quant_groups_kernel<DT, FMT, LPG, CPL, NTS>;
+    const int grid = balanced_grid((int64_t(a.units) + 3) / 4, resident_wgs(kern));
+    kern<<<grid, kThreads, 0, st>>>(a);
+    return check_launch("quant_groups_kernel");
+  }
+  template <int LPG, bool NTS>
+  static int by_cpl(const RowArgs& a, int cpl, hipStream_t st) {
+    if (cpl == 4) return go<LPG, 4, NTS>(a, st);
+    if (cpl == 2) return go<LPG, 2, NTS>(a, st);
+    return go<LPG, 1, NTS>(a, st);
+  }
+  template <bool NTS>
+  static int by_lpg(const RowArgs& a, int lpg, int cpl, hipStream_t st) {
+    switch (lpg) {
+      case 1: return by_cpl<1, NTS>(a, cpl, st);
+      case 2: return by_cpl<2, NTS>(a, cpl, st);
+      case 4: return by_cpl<4, NTS>(a, cpl, st);
+      case 8: return by_cpl<8, NTS>(a, cpl, st);
+      case 16: return by_cpl<16, NTS>(a, cpl, st);
+      case 32: return by_cpl<32, NTS>(a, cpl, st);
+      case 64: return by_cpl<64, NTS>(a, cpl, st);
+      default: return set_error(PCAMD_ERR_UNSUPPORTED, "row kernel: unsupported lanes per group %d", lpg);
     }
-    return check_launch("quant_rows_kernel");
+  }
+  static int run(const RowArgs& a, int lpg, int cpl, hipStream_t st) {
+    return nt_stores() ? by_lpg<true>(a, lpg, cpl, st) : by_lpg<false>(a, lpg, cpl, st);
   }
 };
 
 template <int DT, int FMT>
+struct LaunchRowBlock {
+  template <int CPT, bool NTS>
+  static int go(const RowArgs& a, hipStream_t st) {
+    auto kern = quant_rowblock_kernel<DT, FMT, CPT, NTS>;
+    const int grid = balanced_grid(a.units, resident_wgs(kern));
+    kern<<<grid, kThreads, 0, st>>>(a);
+    return check_launch("quant_rowblock_kernel");
+  }
+  template <int MAXC, bool NTS>
+  static int wave(const RowArgs& a, hipStream_t st) {
+    const int grid = static_cast<int>((int64_t(a.units) + 3) / 4);
+    quant_waverow_kernel<DT, FMT, MAXC, NTS><<<grid, kThreads, 0, st>>>(a);
+    return check_launch("quant_waverow_kernel");
+  }
+  template <bool NTS>
+  static int pick(const RowArgs& a, hipStream_t st) {
+    // rows up to 8192 elements: one wave per row; longer: a workgroup per row
+    if (a.cpl <= 4) return wave<4, NTS>(a, st);
+    if (a.cpl <= 8) return wave<8, NTS>(a, st);
+    if (a.cpl <= 16) return wave<16, NTS>(a, st);
+    const int cpt = (a.chunks + kThreads - 1) / kThreads;
+    if (cpt <= 1) return go<1, NTS>(a, st);
+    if (cpt <= 2) return go<2, NTS>(a, st);
+    if (cpt <= 4) return go<4, NTS>(a, st);
+    return go<8, NTS>(a, st);
+  }
+  static int run(const RowArgs& a, hipStream_t st) { return nt_stores() ? pick<true>(a, st) : pick<false>(a, st); }
+};
+
+template <int DT, int FMT>
 struct LaunchTile {
-  static int run(const TileArgs& a, int lpr, hipStream_t st) {
-    const int grid = grid_for(a.blocks);
-    switch (lpr) {
-      case 4: quant_tile_kernel<DT, FMT, 4><<<grid, kThreads, 0, st>>>(a); break;
-      case 8: quant_tile_kernel<DT, FMT, 8><<<grid, kThreads, 0, st>>>(a); break;
-      case 16: quant_tile_kernel<DT, FMT, 16><<<grid, kThreads, 0, st>>>(a); break;
-      case 32: quant_tile_kernel<DT, FMT, 32><<<grid, kThreads, 0, st>>>(a); break;
-      case 64: quant_tile_kernel<DT, FMT, 64><<<grid, kThreads, 0, st>>>(a); break;
-      default: return set_error(PCAMD_ERR_UNSUPPORTED, "tile kernel: unsupported lanes per row %d", lpr);
-    }
+  template <int CPT, bool NTS>
+  static int go(const TileArgs& a, hipStream_t st) {
+    auto kern = quant_tile_kernel<DT, FMT, CPT, NTS>;
+    const int grid = balanced_grid(a.blocks, resident_wgs(kern));
+    kern<<<grid, kThreads, 0, st>>>(a);
     return check_launch("quant_tile_kernel");
   }
+  template <bool NTS>
+  static int by_cpt(const TileArgs& a, hipStream_t st) {
+    switch (a.cpt) {
+      case 1: return go<1, NTS>(a, st);
+      case 2: return go<2, NTS>(a, st);
+      case 4: return go<4, NTS>(a, st);
+      case 8: return go<8, NTS>(a, st);
+      case 16: return go<16, NTS>(a, st);
+      default: return set_error(PCAMD_ERR_UNSUPPORTED, "tile kernel: unsupported chunks per thread %d", a.cpt);
+    }
+  }
+  static int run(const TileArgs& a, hipStream_t st) { return nt_stores() ? by_cpt<true>(a, st) : by_cpt<false>(a, st); }
 };
 
 template <int DT, int FMT>
@@ -598,33 +786,42 @@ extern "C" int pcamd_quant_block(const void* x, int x_dtype, int64_t batch, int6
   const bool fast = row_fast_ok(x, x_dtype, y, n, sxb, sxm, sxn, syb, sym, syn);
   const int64_t mb = (m + block_m - 1) / block_m, nb = (n + block_n - 1) / block_n;
 
-  if (fast && block_m == 1 && block_n >= 8 && block_n <= 512) {
+  if (fast && block_m == 1 && block_n >= 8 && block_n <= 512 && batch * m < UINT32_MAX / 64 &&
+      m < UINT32_MAX && n / 8 < INT32_MAX / 2) {
     RowArgs a{};
     a.x = static_cast<const char*>(x); a.y = static_cast<uint8_t*>(y); a.scale = scale;
-    a.m = m; a.sxb = sxb; a.sxm = sxm; a.syb = syb; a.sym = sym;
+    a.m = static_cast<uint32_t>(m); a.sxb = sxb; a.sxm = sxm; a.syb = syb; a.sym = sym;
     a.ssb = ssb; a.ssm = ssm; a.ssn = ssn;
     a.chunks = static_cast<int32_t>(n / 8);
     const int lpg = static_cast<int>(block_n / 8);
-    int cpl = static_cast<int>(std::min<int64_t>(kMaxSlots, (a.chunks + 63) / 64));
-    cpl = std::max(cpl, 1);
+    // largest unit (chunk slots per lane) that wastes at most 1/16 of the lanes
+    int cpl = 1;
+    for (int c : {4, 2}) {
+      const int64_t span = 64LL * c, padded = (a.chunks + span - 1) / span * span;
+      if ((padded - a.chunks) * 16 <= a.chunks) { cpl = c; break; }
+    }
     a.cpl = cpl;
-    a.segs = static_cast<int32_t>((a.chunks + 64LL * cpl - 1) / (64LL * cpl));
-    a.units = batch * m * a.segs;
+    a.segs = static_cast<uint32_t>((a.chunks + 64LL * cpl - 1) / (64LL * cpl));
+    a.units = static_cast<uint32_t>(batch * m * a.segs);
     a.fp8_max = fp8_max; a.eps = eps;
-    if (n / 8 > INT32_MAX) return set_error(PCAMD_ERR_UNSUPPORTED, "row too long");
-    return dispatch_dt_fmt<LaunchRows>(x_dtype, y_dtype, a, lpg, false, st);
+    if (int64_t(batch) * m * a.segs < UINT32_MAX) return dispatch_dt_fmt<LaunchGroups>(x_dtype, y_dtype, a, lpg, cpl, st);
   }
   const int64_t lpr = block_n / 8;
   if (fast && block_n >= 32 && lpr <= 64 && (block_m * lpr) % kThreads == 0 &&
-      block_m * lpr / kThreads <= kMaxSlots) {
+      block_m * lpr / kThreads <= kMaxSlots && batch * mb * nb < UINT32_MAX) {
     TileArgs a{};
     a.x = static_cast<const char*>(x); a.y = static_cast<uint8_t*>(y); a.scale = scale;
     a.m = m; a.n = n; a.sxb = sxb; a.sxm = sxm; a.syb = syb; a.sym = sym;
-    a.ssb = ssb; a.ssm = ssm; a.ssn = ssn; a.mb = mb; a.nb = nb; a.blocks = batch * mb * nb;
+    a.ssb = ssb; a.ssm = ssm; a.ssn = ssn;
+    a.mb = static_cast<uint32_t>(mb); a.nb = static_cast<uint32_t>(nb);
+    a.blocks = static_cast<uint32_t>(batch * mb * nb);
     a.block_m = static_cast<int32_t>(block_m);
     a.cpt = static_cast<int32_t>(block_m * lpr / kThreads);
+    a.lpr = static_cast<int32_t>(lpr);
+    a.lpr_shift = 0;
+    while ((1 << a.lpr_shift) < a.lpr) ++a.lpr_shift;
     a.fp8_max = fp8_max; a.eps = eps;
-    return dispatch_dt_fmt<LaunchTile>(x_dtype, y_dtype, a, static_cast<int>(lpr), st);
+    return dispatch_dt_fmt<LaunchTile>(x_dtype, y_dtype, a, st);
   }
   if (fast && block_n == 1 && block_m >= 16 && block_m <= 256) {
     ColArgs a{};
@@ -675,17 +872,17 @@ extern "C" int pcamd_quant_channel(const void* x, int x_dtype, int64_t batch, in
     a.fp8_max = fp8_max; a.eps = eps;
     return dispatch_dt_fmt<LaunchGeneric>(x_dtype, y_dtype, a, 2, st);
   }
-  if (channel_axis == -2 && fast && n / 8 <= 64LL * kMaxSlots) {
+  if (channel_axis == -2 && fast && n / 8 <= 8LL * kThreads && batch * m < UINT32_MAX && m < UINT32_MAX) {
     RowArgs a{};
     a.x = static_cast<const char*>(x); a.y = static_cast<uint8_t*>(y); a.scale = scale;
-    a.m = m; a.sxb = sxb; a.sxm = sxm; a.syb = syb; a.sym = sym;
+    a.m = static_cast<uint32_t>(m); a.sxb = sxb; a.sxm = sxm; a.syb = syb; a.sym = sym;
     a.ssb = ssb; a.ssm = ssc; a.ssn = 0;
     a.chunks = static_cast<int32_t>(n / 8);
-    a.cpl = std::max(1, static_cast<int>((a.chunks + 63) / 64));
+    a.cpl = static_cast<int32_t>((a.chunks + 63) / 64);  // chunk slots per lane, wave-per-row
     a.segs = 1;
-    a.units = batch * m;
+    a.units = static_cast<uint32_t>(batch * m);
     a.fp8_max = fp8_max; a.eps = eps;
-    return dispatch_dt_fmt<LaunchRows>(x_dtype, y_dtype, a, 64, true, st);
+    return dispatch_dt_fmt<LaunchRowBlock>(x_dtype, y_dtype, a, st);
   }
   if (channel_axis == -1 && fast) {
     ColArgs a{};
