@@ -492,7 +492,10 @@ extern "C" int pcamd_bmm_scaled(const void* a, const void* b, int ab_dtype, int6
   // tuned path: K a multiple of 128, 16-byte aligned operands and rows,
   // power-of-two block sizes, 32-bit addressable batch slices
   {
-    const int64_t TM = bmm_fast_tile_m(), TN = bmm_fast_tile_n();
+    const bool wide = k >= 256 && (scale_mode != PCAMD_SCALE_BLOCK || args.qbk == 128) &&
+                      !(getenv("PCAMD_BMM_WIDE") && getenv("PCAMD_BMM_WIDE")[0] == '0');
+    const int64_t TM = wide ? bmm_wide_tile() : bmm_fast_tile_m();
+    const int64_t TN = wide ? bmm_wide_tile() : bmm_fast_tile_n();
     const int64_t tm = (m + TM - 1) / TM, tn = (n + TN - 1) / TN;
     const int64_t lda = a_k ? sam : sak, ldb = b_k ? sbn : sbk;
     // largest byte offset a workgroup can form (rows padded to the tile)
@@ -523,6 +526,7 @@ extern "C" int pcamd_bmm_scaled(const void* a, const void* b, int ab_dtype, int6
       const int fmode = scale_mode == PCAMD_SCALE_BLOCK ? 0 : scale_mode == PCAMD_SCALE_CHANNEL ? 1 : 2;
       const bool sb_col = scale_mode == PCAMD_SCALE_BLOCK && args.qbn < 16;
       const bool qb1 = scale_mode == PCAMD_SCALE_BLOCK && args.qbk == 128;
+      if (wide) return bmm_wide_launch(f, ab_dtype, a_k, b_k, fmode, sb_col, st);
       return bmm_fast_launch(f, ab_dtype, a_k, b_k, fmode, sb_col, qb1, st);
     }
   }

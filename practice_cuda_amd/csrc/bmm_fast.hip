@@ -390,6 +390,134 @@ __global__ __launch_bounds__(NT, 1) void bmm_fast_kernel(FastArgs a) {
   }
 }
 
+// K <= 128 (one K step, one quant-K block): a single LDS stage (48 KiB), the
+// MFMA result is scaled once in the epilogue (acc = P * sa * sb for block
+// scales), and two workgroups share a CU so one's stores overlap the other's
+// loads and MFMAs. This is the output-bound config-4 shape.
+template <bool A_K, bool B_K, int FMT, int MODE, bool SB_COL>
+__global__ __launch_bounds__(NT, 2) void bmm_single_kernel(FastArgs a) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  const int t = threadIdx.x;
+  const int lane = t & 63, wave = t >> 6;
+  const int wm = wave & 1, wn = wave >> 1;
+  const int lr = lane & 15, lg = lane >> 4;
+
+  int pid = blockIdx.x;
+  if ((a.total_tiles & 7) == 0) pid = (pid & 7) * (a.total_tiles >> 3) + (pid >> 3);
+  const int bidx = pid / a.tiles_per_batch;
+  const int tile = pid - bidx * a.tiles_per_batch;
+  constexpr int GROUP_M = 8;
+  const int per_group = GROUP_M * a.tiles_n;
+  const int group = tile / per_group;
+  const int first_m = group * GROUP_M;
+  const int gm = min(a.tiles_m - first_m, GROUP_M);
+  const int in_group = tile - group * per_group;
+  const int m0 = (first_m + in_group % gm) * BM;
+  const int n0 = (in_group / gm) * BN;
+
+  const __amdgpu_buffer_rsrc_t rsa = make_rsrc(a.a + bidx * a.sab, a.a_extent);
+  const __amdgpu_buffer_rsrc_t rsb = make_rsrc(a.b + bidx * a.sbb, a.b_extent);
+  if constexpr (A_K) issue_kmajor<BM>(rsa, smem, m0, a.lda, 0, wave, lane);
+  if constexpr (B_K) issue_kmajor<BN>(rsb, smem + A_BYTES, n0, a.ldb, 0, wave, lane);
+  if constexpr (!A_K) {
+    MNStage<BM> st;
+    st.load(rsa, m0, a.lda, 0, t);
+    st.store(smem, t);
+  }
+  if constexpr (!B_K) {
+    MNStage<BN> st;
+    st.load(rsb, n0, a.ldb, 0, t);
+    st.store(smem + A_BYTES, t);
+  }
+
+  const int row_base = m0 + wm * 64 + lr;
+  const int col_base = n0 + wn * 128 + 4 * lg;
+  // per-row and per-column scales (issued before the wait so they overlap it)
+  float sav[4], sbv[8][SB_COL || MODE == 1 ? 4 : 1];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int mm = row_base + 16 * i;
+    if constexpr (MODE == 0) sav[i] = mm < a.m ? a.sa[bidx * a.ssab + int64_t(mm >> a.qbm_shift) * a.ssa1] : 0.0f;
+    else if constexpr (MODE == 1) sav[i] = mm < a.m ? a.sa[bidx * a.ssab + int64_t(mm) * a.ssa1] : 0.0f;
+    else sav[i] = 1.0f;
+  }
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    if constexpr (MODE == 0 && !SB_COL) {
+      const int nn = col_base + 16 * j;
+      sbv[j][0] = nn < a.n ? a.sb[bidx * a.ssbb + int64_t(nn >> a.qbn_shift) * a.ssb2] : 0.0f;
+    } else if constexpr (MODE == 0 || MODE == 1) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int nn = col_base + 16 * j + r;
+        if (nn < a.n) {
+          sbv[j][r] = MODE == 0 ? a.sb[bidx * a.ssbb + int64_t(nn >> a.qbn_shift) * a.ssb2]
+                                : a.sb[bidx * a.ssbb + int64_t(nn) * a.ssb1];
+        } else {
+          sbv[j][r] = 0.0f;
+        }
+      }
+    } else {
+      sbv[j][0] = 1.0f;
+    }
+  }
+
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+
+  v4f acc[4][8];
+  {
+    v8i af[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) af[i] = frag(smem, wm * 64 + i * 16 + lr, lg);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const v8i bf = frag(smem + A_BYTES, wn * 128 + j * 16 + lr, lg);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc[i][j] = mfma<FMT>(bf, af[i], v4f{0.f, 0.f, 0.f, 0.f});
+    }
+  }
+
+  float tscale = 1.0f;
+  if constexpr (MODE == 2) tscale = a.scales_are_quant ? 1.0f / (a.sa[0] * a.sb[0]) : a.sa[0];
+  const bool plain = a.bias == nullptr && a.act == PCAMD_ACT_NONE && a.c_dtype == kBF16;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int mm = row_base + 16 * i;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int nn = col_base + 16 * j;
+      float v[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        float s;
+        if constexpr (MODE == 0) s = sav[i] * sbv[j][SB_COL ? r : 0];  // (sa * sb), then * P
+        else if constexpr (MODE == 1) {
+          s = sav[i] * sbv[j][r];
+          if (a.scales_are_quant) s = 1.0f / s;
+        } else s = tscale;
+        v[r] = acc[i][j][r] * s;
+      }
+      if (mm >= a.m || nn >= a.n) continue;
+      __bf16* p = reinterpret_cast<__bf16*>(a.c) + bidx * a.scb + int64_t(mm) * a.scm + nn;
+      if (plain && nn + 4 <= a.n && (reinterpret_cast<uintptr_t>(p) & 7) == 0) {
+        *reinterpret_cast<uint2*>(p) = make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
+      } else {
+        epilogue_general(a.c, bidx * a.scb + int64_t(mm) * a.scm, a.c_dtype, a.bias,
+                         bidx * a.sbiasb + int64_t(mm) * a.sbiasm, a.sbiasn, a.bias_dtype, a.act, nn,
+                         min(4, a.n - nn), v[0], v[1], v[2], v[3]);
+      }
+    }
+  }
+}
+
+template <bool A_K, bool B_K, int FMT, int MODE, bool SB_COL>
+int launch_single(const FastArgs& a, hipStream_t st) {
+  auto kern = bmm_single_kernel<A_K, B_K, FMT, MODE, SB_COL>;
+  kern<<<a.total_tiles, NT, STAGE, st>>>(a);
+  return check_launch("bmm_single_kernel");
+}
+
 template <bool A_K, bool B_K, int FMT, int MODE, bool SB_COL, bool QB1>
 int launch_one(const FastArgs& a, hipStream_t st) {
   auto kern = bmm_fast_kernel<A_K, B_K, FMT, MODE, SB_COL, QB1>;
@@ -406,6 +534,11 @@ int launch_one(const FastArgs& a, hipStream_t st) {
 
 template <bool A_K, bool B_K, int FMT>
 int launch_mode(const FastArgs& a, int mode, bool sb_col, bool qb1, hipStream_t st) {
+  if (a.k == BK) {  // one K step: single-stage kernel, two workgroups per CU
+    if (mode == 1) return launch_single<A_K, B_K, FMT, 1, false>(a, st);
+    if (mode == 2) return launch_single<A_K, B_K, FMT, 2, false>(a, st);
+    return sb_col ? launch_single<A_K, B_K, FMT, 0, true>(a, st) : launch_single<A_K, B_K, FMT, 0, false>(a, st);
+  }
   if (mode == 1) return launch_one<A_K, B_K, FMT, 1, false, false>(a, st);
   if (mode == 2) return launch_one<A_K, B_K, FMT, 2, false, false>(a, st);
   if (sb_col) {

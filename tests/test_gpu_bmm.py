@@ -55,7 +55,8 @@ def rand(shape, seed, scale=1.0):
     return (torch.randn(*shape, generator=g) * scale).bfloat16()
 
 
-SHAPES = [(2, 128, 128, 128), (3, 33, 47, 65), (3, 129, 131, 127), (2, 256, 384, 512), (1, 64, 96, 1024)]
+SHAPES = [(2, 128, 128, 128), (3, 33, 47, 65), (3, 129, 131, 127), (2, 256, 384, 512), (1, 64, 96, 1024),
+          (2, 272, 528, 384)]
 
 
 @pytest.mark.parametrize("scheme", SCHEMES)
