@@ -53,9 +53,21 @@ constexpr int A_BYTES = BM * BK, B_BYTES = BN * BK;  // 32 KiB each
 constexpr int STAGE = A_BYTES + B_BYTES;
 constexpr uint32_t kRsrcWord3 = 0x00020000u;
 
-// K-major swizzle: chunk c of row r sits at position c ^ (r & 7), so the 8
-// rows one ds_read_b128 pass serves hit 8 different 16-byte bank groups.
-PCAMD_DEV int swz_k(int r) { return r & 7; }
+// LDS swizzles. gfx950's LDS serves 256 bytes (64 banks) per cycle.
+// K-major tile (128-byte rows): chunk c of row r sits at position c ^ swz_k(r).
+// A fragment read touches rows r0..r0+15 (lanes 16 g + r) at chunk 2 g + h.
+// Measured on gfx950, XOR-ing with r & 7 or with (r >> 1) & 7 both leave every
+// ds_read_b128 2-way conflicted: the lanes served together are not 16
+// consecutive ones but (among the groupings that fit) eight rows of two
+// adjacent g. swz_k = 5 * bit1(r) ^ bit2(r) spreads the 16 (row, chunk) pairs
+// of each such group over distinct bank groups for all of them.
+PCAMD_DEV int swz_k(int r) { return (((r >> 1) & 1) * 5) ^ ((r >> 2) & 1); }
+// MN-major tile (256-byte k-rows): chunk c of k-row k sits at position
+// c ^ (k & 7) ^ (8 ((k >> 5) & 1)). A 16-lane group reads 8 k-rows k0..k0+7
+// (k0 % 8 == 0) at one 8-byte half pair: k & 7 spreads them over 32 banks,
+// and the group served in the same cycle (k-rows 32 further on) lands in the
+// other 32.
+PCAMD_DEV int swz_mn(int k) { return (k & 7) ^ (((k >> 5) & 1) << 3); }
 
 // Buffer descriptor in four SGPRs: base, byte size (the hardware returns 0
 // for offsets at or past it), raw addressing.
@@ -93,18 +105,18 @@ PCAMD_DEV void lds_dma16(v4i rs, uint32_t lds, uint32_t voff) {
 // cannot hoist one loop-invariant VGPR per instruction out of the K loop.
 //
 // K-major tile: ROWS rows (row0 + r, stride ld) x 128 k-bytes. Instruction i
-// of wave w fills rows w * ROWS / 8 + 8 i + (lane >> 3), lane & 7 being the
-// LDS slot within the row; the slot holds global chunk slot ^ (r & 7), and
-// r & 7 == lane >> 3.
+// of wave w fills rows rb = w * ROWS / 8 + 8 i .. rb + 7, lane l taking row
+// rb + (l >> 3) and LDS slot l & 7, which holds global chunk
+// (l & 7) ^ swz_k(r). rb is a multiple of 8 and swz_k reads only bits 1-2 of
+// r, so swz_k(r) = swz_k(l >> 3) and one lane offset serves every instruction.
 template <int ROWS>
 struct KMajorLoader {
   static constexpr int PER_WAVE = ROWS / WAVES;
   static constexpr int INSTS = PER_WAVE / 8;
   uint32_t voff;
-  PCAMD_DEV KMajorLoader(uint32_t ld, int lane)
-      : voff((lane >> 3) * ld + (((lane & 7) ^ (lane >> 3)) << 4)) {}
-  PCAMD_DEV void issue(v4i rs, uint8_t* tile, uint32_t row0, uint32_t ld, uint32_t k0,
-                       int wave) const {
+  PCAMD_DEV KMajorLoader(uint32_t ld, int lane, int /*wave*/)
+      : voff((lane >> 3) * ld + (((lane & 7) ^ swz_k(lane >> 3)) << 4)) {}
+  PCAMD_DEV void issue(v4i rs, uint8_t* tile, uint32_t row0, uint32_t ld, uint32_t k0, int wave) const {
 #pragma unroll
     for (int i = 0; i < INSTS; ++i) {
       const int rb = wave * PER_WAVE + i * 8;
@@ -116,27 +128,27 @@ struct KMajorLoader {
 };
 
 // MN-major tile: 128 k-rows (k0 + k, stride ld) x COLS bytes from col0.
-// Instruction i of wave w fills k-rows kb = w * 16 + i * R .. + R (R = 64 /
-// (COLS / 16) rows per instruction); lane l takes k-row kb + l / CHUNKS, slot
-// l % CHUNKS, global chunk slot ^ (k & 7). kb & 7 takes the values 0 and R & 7
-// alternately, so two lane offsets serve all instructions.
+// Instruction i of wave w fills k-rows kb = w * 16 + i * R .. + R - 1 (R = 64 /
+// (COLS / 16) rows per instruction); lane l takes k-row kb + l / CHUNKS and LDS
+// slot l % CHUNKS, which holds global chunk slot ^ swz_mn(k). Bit 5 of k is
+// the wave's (w * 16 + i * R + l / CHUNKS < w * 16 + 16), and k & 7 repeats
+// every two instructions, so two lane offsets per wave serve them all.
 template <int COLS>
 struct MNMajorLoader {
   static constexpr int CHUNKS = COLS / 16;
   static constexpr int R = 64 / CHUNKS;
   static constexpr int PER_WAVE = BK / WAVES;
   static constexpr int INSTS = PER_WAVE / R;
+  static_assert(COLS == 256 && PER_WAVE == 16, "swizzle assumes 256-byte k-rows, 16 per wave");
   uint32_t voff[2];
-  PCAMD_DEV MNMajorLoader(uint32_t ld, int lane) {
+  PCAMD_DEV MNMajorLoader(uint32_t ld, int lane, int wave) {
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
-      const int k = h * R + lane / CHUNKS;
-      voff[h] = (lane / CHUNKS) * ld + (((lane % CHUNKS) ^ (k & 7)) << 4);
+      const int k = wave * PER_WAVE + h * R + lane / CHUNKS;
+      voff[h] = (lane / CHUNKS) * ld + (((lane % CHUNKS) ^ swz_mn(k)) << 4);
     }
   }
-  PCAMD_DEV void issue(v4i rs, uint8_t* tile, uint32_t col0, uint32_t ld, uint32_t k0,
-                       int wave) const {
-    static_assert((PER_WAVE % 8) == 0 && (2 * R) % 8 == 0, "k-row phase must repeat every two instructions");
+  PCAMD_DEV void issue(v4i rs, uint8_t* tile, uint32_t col0, uint32_t ld, uint32_t k0, int wave) const {
 #pragma unroll
     for (int i = 0; i < INSTS; ++i) {
       const int kb = wave * PER_WAVE + i * R;
@@ -170,7 +182,7 @@ PCAMD_DEV v8i frag_mn(const uint8_t* tile, int col16, int lane) {
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
     const int k = 32 * g + 8 * q + (j >> 1);
-    const uint8_t* p = tile + k * COLS + ((c ^ (k & 7)) << 4) + half;
+    const uint8_t* p = tile + k * COLS + ((c ^ swz_mn(k)) << 4) + half;
     const v2i v = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i_ptr)(p));
     f[2 * q] = v[0];
     f[2 * q + 1] = v[1];
@@ -253,8 +265,8 @@ __global__ __launch_bounds__(NT, 1) void bmm_wide_kernel(FastArgs a) {
   const v4i rsb = make_rsrc(a.b + bidx * a.sbb, a.b_extent);
   using LA = typename std::conditional<A_K, KMajorLoader<BM>, MNMajorLoader<BM>>::type;
   using LB = typename std::conditional<B_K, KMajorLoader<BN>, MNMajorLoader<BN>>::type;
-  const LA load_a(a.lda, lane);
-  const LB load_b(a.ldb, lane);
+  const LA load_a(a.lda, lane, wave);
+  const LB load_b(a.ldb, lane, wave);
 
   auto issue = [&](int ks, uint8_t* stage) {
     const uint32_t k0 = ks * BK;
@@ -360,28 +372,94 @@ __global__ __launch_bounds__(NT, 1) void bmm_wide_kernel(FastArgs a) {
   // ---- epilogue ----
   float tscale = 1.0f;
   if constexpr (MODE == 2) tscale = a.scales_are_quant ? 1.0f / (a.sa[0] * a.sb[0]) : a.sa[0];
+  // output value (i, j, r) of this lane with the channel / tensor scales applied
+  // column scales of sub-tile column j (channel mode; 1 otherwise)
+  auto col_scales = [&](int j, float (&sbv)[4]) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      sbv[r] = 1.0f;
+      if constexpr (MODE == 1) {
+        const int nn = col_base + 16 * j + r;
+        sbv[r] = nn < a.n ? a.sb[bidx * a.ssbb + int64_t(nn) * a.ssb1] : 0.0f;
+      }
+    }
+  };
+  auto out_value = [&](int i, int j, int r, float sam_v, const float (&sbv)[4]) -> float {
+    float x = acc[i][j][r];
+    if constexpr (MODE == 1) {
+      float s = sam_v * sbv[r];
+      if (a.scales_are_quant) s = 1.0f / s;
+      x *= s;
+    } else if constexpr (MODE == 2) {
+      x *= tscale;
+    }
+    return x;
+  };
+  auto row_scale = [&](int i) -> float {
+    float sam_v = 1.0f;
+    if constexpr (MODE == 1) {
+      const int mm = row_base + 16 * i;
+      sam_v = mm < a.m ? a.sa[bidx * a.ssab + int64_t(mm) * a.ssa1] : 0.0f;
+    }
+    return sam_v;
+  };
   const bool plain = a.bias == nullptr && a.act == PCAMD_ACT_NONE && a.c_dtype == kBF16;
+  const bool staged = plain && (a.n & 7) == 0 && (a.scm & 7) == 0 && (a.scb & 7) == 0 &&
+                      (reinterpret_cast<uintptr_t>(a.c) & 15) == 0;
+  if (staged) {
+    // A lane's MFMA outputs are 4 columns of one row, so direct stores write
+    // 32-byte pieces of 16 rows per instruction. Instead each wave stages half
+    // of its 64 x 128 sub-tile (32 rows x 256 bytes) in 8 KiB of the LDS stage
+    // the last K step did not read (no other wave touches it, so no barrier),
+    // then stores 16 bytes per lane: 4 rows x 256 contiguous bytes per
+    // instruction, full 128-byte lines, non-temporal (C is not re-read).
+    // Staged chunk c of row r sits at position c ^ (r & 15).
+    typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+    uint8_t* stg = smem + (ksteps & 1) * STAGE + wave * 8192;
+    __bf16* cbase = reinterpret_cast<__bf16*>(a.c) + bidx * a.scb;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const float sam_v[2] = {row_scale(2 * h), row_scale(2 * h + 1)};
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        float sbv[4];
+        col_scales(j, sbv);
+#pragma unroll
+        for (int il = 0; il < 2; ++il) {
+          const int i = 2 * h + il;
+          const int r = 16 * il + lr;
+          const int chunk = 2 * j + (lg >> 1);
+          uint2* dst = reinterpret_cast<uint2*>(stg + r * 256 + ((chunk ^ (r & 15)) << 4) + ((lg & 1) << 3));
+          *dst = make_uint2(pack_bf16x2(out_value(i, j, 0, sam_v[il], sbv), out_value(i, j, 1, sam_v[il], sbv)),
+                            pack_bf16x2(out_value(i, j, 2, sam_v[il], sbv), out_value(i, j, 3, sam_v[il], sbv)));
+        }
+      }
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+      for (int it = 0; it < 8; ++it) {
+        const int r = 4 * it + (lane >> 4);
+        const int chunk = lane & 15;
+        const u32x4 v = *reinterpret_cast<const u32x4*>(stg + r * 256 + ((chunk ^ (r & 15)) << 4));
+        const int mm = m0 + wm * 64 + 32 * h + r;
+        const int nn = n0 + wn * 128 + 8 * chunk;
+        if (mm < a.m && nn < a.n) __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(cbase + int64_t(mm) * a.scm + nn));
+      }
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    }
+    return;
+  }
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int mm = row_base + 16 * i;
-    float sam_v = 1.0f;
-    if constexpr (MODE == 1) sam_v = mm < a.m ? a.sa[bidx * a.ssab + int64_t(mm) * a.ssa1] : 0.0f;
+    const float sam_v = row_scale(i);
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       const int nn = col_base + 16 * j;
+      float sbv[4];
+      col_scales(j, sbv);
       float v[4];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        float x = acc[i][j][r];
-        if constexpr (MODE == 1) {
-          float s = nn + r < a.n ? sam_v * a.sb[bidx * a.ssbb + int64_t(nn + r) * a.ssb1] : 0.0f;
-          if (a.scales_are_quant) s = 1.0f / s;
-          x *= s;
-        } else if constexpr (MODE == 2) {
-          x *= tscale;
-        }
-        v[r] = x;
-      }
+      for (int r = 0; r < 4; ++r) v[r] = out_value(i, j, r, sam_v, sbv);
       if (mm >= a.m || nn >= a.n) continue;
       __bf16* p = reinterpret_cast<__bf16*>(a.c) + bidx * a.scb + int64_t(mm) * a.scm + nn;
       if (plain && nn + 4 <= a.n && (reinterpret_cast<uintptr_t>(p) & 7) == 0) {
