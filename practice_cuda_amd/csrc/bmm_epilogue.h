@@ -1,0 +1,72 @@
+// bmm_epilogue.h - LDS-staged bf16 output of one wave's 64 x 128 sub-tile.
+//
+// With the MFMA operands swapped, a lane holds 4 consecutive columns of one
+// row per 16 x 16 tile, so direct stores write 32-byte pieces of 16 rows per
+// instruction (16 partial-line requests each). Staging through LDS lets each
+// lane store 16 contiguous bytes instead: an instruction covers 4 rows x 256
+// contiguous bytes, i.e. full 128-byte lines. The stores are non-temporal:
+// C is written once and should not evict the operand tiles from L2.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "fp8_common.h"
+
+namespace pcamd {
+
+PCAMD_DEV uint32_t pack_bf16_pair(float lo, float hi) {
+  return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<__bf16>(lo))) |
+         (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<__bf16>(hi))) << 16);
+}
+
+// Whether the staged path applies: bf16 output without bias or activation,
+// 16-byte aligned rows and N a multiple of 8 (a lane's 8 columns never
+// straddle N).
+PCAMD_DEV bool staged_output_ok(const void* c, int64_t scb, int64_t scm, int n, bool plain) {
+  return plain && (n & 7) == 0 && (scm & 7) == 0 && (scb & 7) == 0 && (reinterpret_cast<uintptr_t>(c) & 15) == 0;
+}
+
+// stg: 8 KiB of LDS private to this wave. c: the batch's C (bf16, row pitch
+// scm elements). The sub-tile covers rows row0 .. row0 + 63 and columns
+// col0 .. col0 + 127; value(i, j, v) fills the 4 outputs of this lane in
+// MFMA tile (i, j): row row0 + 16 i + (lane & 15), columns
+// col0 + 16 j + 4 (lane >> 4) + r. The sub-tile goes out in two halves of
+// 32 rows; staged chunk c of row r sits at LDS position c ^ (r & 15).
+template <typename ValueFn>
+PCAMD_DEV void store_subtile_staged(uint8_t* stg, __bf16* c, int64_t scm, int m, int n, int row0, int col0,
+                                    int lane, ValueFn&& value) {
+  typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+  const int lr = lane & 15, lg = lane >> 4;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+#pragma unroll
+      for (int il = 0; il < 2; ++il) {
+        float v[4];
+        value(2 * h + il, j, v);
+        const int r = 16 * il + lr;
+        const int chunk = 2 * j + (lg >> 1);
+        uint2* dst = reinterpret_cast<uint2*>(stg + r * 256 + ((chunk ^ (r & 15)) << 4) + ((lg & 1) << 3));
+        *dst = make_uint2(pack_bf16_pair(v[0], v[1]), pack_bf16_pair(v[2], v[3]));
+      }
+    }
+    // LDS operations of one wave complete in order; the wait keeps the
+    // compiler from moving the reads above the writes.
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+    for (int it = 0; it < 8; ++it) {
+      const int r = 4 * it + (lane >> 4);
+      const int chunk = lane & 15;
+      const u32x4 v = *reinterpret_cast<const u32x4*>(stg + r * 256 + ((chunk ^ (r & 15)) << 4));
+      const int mm = row0 + 32 * h + r;
+      const int nn = col0 + 8 * chunk;
+      if (mm < m && nn < n) __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(c + int64_t(mm) * scm + nn));
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  }
+}
+
+}  // namespace pcamd

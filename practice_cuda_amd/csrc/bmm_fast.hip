@@ -31,6 +31,7 @@
 #include <cstdint>
 
 #include "abi_util.h"
+#include "bmm_epilogue.h"
 #include "bmm_fast.h"
 #include "fp8_common.h"
 
@@ -356,27 +357,43 @@ __global__ __launch_bounds__(NT, 1) void bmm_fast_kernel(FastArgs a) {
   float tscale = 1.0f;
   if constexpr (MODE == 2) tscale = a.scales_are_quant ? 1.0f / (a.sa[0] * a.sb[0]) : a.sa[0];
   const bool plain = a.bias == nullptr && a.act == PCAMD_ACT_NONE && a.c_dtype == kBF16;
+  float sam[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int mm = row_base + 16 * i;
-    float sam_v = 1.0f;
-    if constexpr (MODE == 1) sam_v = mm < a.m ? a.sa[bidx * a.ssab + int64_t(mm) * a.ssa1] : 0.0f;
+    sam[i] = 1.0f;
+    if constexpr (MODE == 1) sam[i] = mm < a.m ? a.sa[bidx * a.ssab + int64_t(mm) * a.ssa1] : 0.0f;
+  }
+  auto value = [&](int i, int j, float (&v)[4]) {
+    const int nn = col_base + 16 * j;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      float x = acc[i][j][r];
+      if constexpr (MODE == 1) {
+        float s = nn + r < a.n ? sam[i] * a.sb[bidx * a.ssbb + int64_t(nn + r) * a.ssb1] : 0.0f;
+        if (a.scales_are_quant) s = 1.0f / s;
+        x *= s;
+      } else if constexpr (MODE == 2) {
+        x *= tscale;
+      }
+      v[r] = x;
+    }
+  };
+  if (staged_output_ok(a.c, a.scb, a.scm, a.n, plain)) {
+    // the stage the last K step did not read is free (every wave passed the
+    // last barrier after its final read of it): 8 KiB of it per wave
+    store_subtile_staged(smem + (ksteps & 1) * STAGE + wave * 8192, reinterpret_cast<__bf16*>(a.c) + bidx * a.scb,
+                         a.scm, a.m, a.n, m0 + wm * 64, n0 + wn * 128, lane, value);
+    return;
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int mm = row_base + 16 * i;
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       const int nn = col_base + 16 * j;
       float v[4];
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        float x = acc[i][j][r];
-        if constexpr (MODE == 1) {
-          float s = nn + r < a.n ? sam_v * a.sb[bidx * a.ssbb + int64_t(nn + r) * a.ssb1] : 0.0f;
-          if (a.scales_are_quant) s = 1.0f / s;
-          x *= s;
-        } else if constexpr (MODE == 2) {
-          x *= tscale;
-        }
-        v[r] = x;
-      }
+      value(i, j, v);
       if (mm >= a.m || nn >= a.n) continue;
       __bf16* p = reinterpret_cast<__bf16*>(a.c) + bidx * a.scb + int64_t(mm) * a.scm + nn;
       if (plain && nn + 4 <= a.n && (reinterpret_cast<uintptr_t>(p) & 7) == 0) {
@@ -481,6 +498,24 @@ __global__ __launch_bounds__(NT, 2) void bmm_single_kernel(FastArgs a) {
   float tscale = 1.0f;
   if constexpr (MODE == 2) tscale = a.scales_are_quant ? 1.0f / (a.sa[0] * a.sb[0]) : a.sa[0];
   const bool plain = a.bias == nullptr && a.act == PCAMD_ACT_NONE && a.c_dtype == kBF16;
+  auto value = [&](int i, int j, float (&v)[4]) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      float s;
+      if constexpr (MODE == 0) s = sav[i] * sbv[j][SB_COL ? r : 0];  // (sa * sb), then * P
+      else if constexpr (MODE == 1) {
+        s = sav[i] * sbv[j][r];
+        if (a.scales_are_quant) s = 1.0f / s;
+      } else s = tscale;
+      v[r] = acc[i][j][r] * s;
+    }
+  };
+  if (staged_output_ok(a.c, a.scb, a.scm, a.n, plain)) {
+    __syncthreads();  // every wave has read its fragments: the stage is free
+    store_subtile_staged(smem + wave * 8192, reinterpret_cast<__bf16*>(a.c) + bidx * a.scb, a.scm, a.m, a.n,
+                         m0 + wm * 64, n0 + wn * 128, lane, value);
+    return;
+  }
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int mm = row_base + 16 * i;
@@ -488,16 +523,7 @@ __global__ __launch_bounds__(NT, 2) void bmm_single_kernel(FastArgs a) {
     for (int j = 0; j < 8; ++j) {
       const int nn = col_base + 16 * j;
       float v[4];
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        float s;
-        if constexpr (MODE == 0) s = sav[i] * sbv[j][SB_COL ? r : 0];  // (sa * sb), then * P
-        else if constexpr (MODE == 1) {
-          s = sav[i] * sbv[j][r];
-          if (a.scales_are_quant) s = 1.0f / s;
-        } else s = tscale;
-        v[r] = acc[i][j][r] * s;
-      }
+      value(i, j, v);
       if (mm >= a.m || nn >= a.n) continue;
       __bf16* p = reinterpret_cast<__bf16*>(a.c) + bidx * a.scb + int64_t(mm) * a.scm + nn;
       if (plain && nn + 4 <= a.n && (reinterpret_cast<uintptr_t>(p) & 7) == 0) {

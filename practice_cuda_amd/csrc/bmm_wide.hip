@@ -33,6 +33,7 @@
 #include <type_traits>
 
 #include "abi_util.h"
+#include "bmm_epilogue.h"
 #include "bmm_fast.h"
 #include "fp8_common.h"
 
@@ -404,48 +405,18 @@ __global__ __launch_bounds__(NT, 1) void bmm_wide_kernel(FastArgs a) {
     return sam_v;
   };
   const bool plain = a.bias == nullptr && a.act == PCAMD_ACT_NONE && a.c_dtype == kBF16;
-  const bool staged = plain && (a.n & 7) == 0 && (a.scm & 7) == 0 && (a.scb & 7) == 0 &&
-                      (reinterpret_cast<uintptr_t>(a.c) & 15) == 0;
-  if (staged) {
-    // A lane's MFMA outputs are 4 columns of one row, so direct stores write
-    // 32-byte pieces of 16 rows per instruction. Instead each wave stages half
-    // of its 64 x 128 sub-tile (32 rows x 256 bytes) in 8 KiB of the LDS stage
-    // the last K step did not read (no other wave touches it, so no barrier),
-    // then stores 16 bytes per lane: 4 rows x 256 contiguous bytes per
-    // instruction, full 128-byte lines, non-temporal (C is not re-read).
-    // Staged chunk c of row r sits at position c ^ (r & 15).
-    typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
-    uint8_t* stg = smem + (ksteps & 1) * STAGE + wave * 8192;
-    __bf16* cbase = reinterpret_cast<__bf16*>(a.c) + bidx * a.scb;
+  if (staged_output_ok(a.c, a.scb, a.scm, a.n, plain)) {
+    // each wave stages its sub-tile in 8 KiB of the LDS stage the last K step
+    // did not read (no other wave touches it, so no barrier is needed)
+    const float sam_v[4] = {row_scale(0), row_scale(1), row_scale(2), row_scale(3)};
+    store_subtile_staged(smem + (ksteps & 1) * STAGE + wave * 8192,
+                         reinterpret_cast<__bf16*>(a.c) + bidx * a.scb, a.scm, a.m, a.n, m0 + wm * 64,
+                         n0 + wn * 128, lane, [&](int i, int j, float (&v)[4]) {
+                           float sbv[4];
+                           col_scales(j, sbv);
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const float sam_v[2] = {row_scale(2 * h), row_scale(2 * h + 1)};
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        float sbv[4];
-        col_scales(j, sbv);
-#pragma unroll
-        for (int il = 0; il < 2; ++il) {
-          const int i = 2 * h + il;
-          const int r = 16 * il + lr;
-          const int chunk = 2 * j + (lg >> 1);
-          uint2* dst = reinterpret_cast<uint2*>(stg + r * 256 + ((chunk ^ (r & 15)) << 4) + ((lg & 1) << 3));
-          *dst = make_uint2(pack_bf16x2(out_value(i, j, 0, sam_v[il], sbv), out_value(i, j, 1, sam_v[il], sbv)),
-                            pack_bf16x2(out_value(i, j, 2, sam_v[il], sbv), out_value(i, j, 3, sam_v[il], sbv)));
-        }
-      }
-      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-#pragma unroll
-      for (int it = 0; it < 8; ++it) {
-        const int r = 4 * it + (lane >> 4);
-        const int chunk = lane & 15;
-        const u32x4 v = *reinterpret_cast<const u32x4*>(stg + r * 256 + ((chunk ^ (r & 15)) << 4));
-        const int mm = m0 + wm * 64 + 32 * h + r;
-        const int nn = n0 + wn * 128 + 8 * chunk;
-        if (mm < a.m && nn < a.n) __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(cbase + int64_t(mm) * a.scm + nn));
-      }
-      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-    }
+                           for (int r = 0; r < 4; ++r) v[r] = out_value(i, j, r, sam_v[i], sbv);
+                         });
     return;
   }
 #pragma unroll
