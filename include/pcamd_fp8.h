@@ -86,15 +86,21 @@ int pcamd_quant_channel(const void *x, int x_dtype, int64_t batch, int64_t m,
 
 /*
  * Per-tensor quantization: amax over the whole tensor, s = max(amax, eps),
- * qs = fp8_max / s, scale[0] = 1 / qs, y = fp8_rne(clamp(x * qs)).
- * quant_scale_out (may be NULL) receives qs. Both scalars are device fp32.
- * Replaces impls/triton_per_tensor.py:28-95 and fp8_bmm/fp8_warper.py:9-77.
+ * qs = reciprocal(s) * fp8_max, scale[0] = reciprocal(qs),
+ * y = fp8_rne(clamp(x * qs)). quant_scale_out (may be NULL) receives qs. Both
+ * scalars are device fp32. scale_dtype (PCAMD_F32 / PCAMD_BF16 / PCAMD_F16) is
+ * the dtype the scalar steps are rounded to: PCAMD_F32 for
+ * fp8_training/fp8_bench/impls/triton_per_tensor.py:28-95; the input's dtype
+ * for the legacy kernels/fp8_bmm/fp8_warper.py:9-77, whose torch ops on 0-d
+ * tensors of the input's dtype round every step (the results are then
+ * exactly representable in that dtype).
  */
 int pcamd_quant_tensor(const void *x, int x_dtype, int64_t batch, int64_t m,
                        int64_t n, int64_t sxb, int64_t sxm, int64_t sxn,
                        void *y, int y_dtype, int64_t syb, int64_t sym,
                        int64_t syn, float *scale, float *quant_scale_out,
-                       float fp8_max, float eps, void *stream);
+                       float fp8_max, float eps, int scale_dtype,
+                       void *stream);
 
 /*
  * Scaled FP8 batched GEMM: c[b, m, n] = act(sum_k a[b, m, k] b[b, k, n] *

@@ -17,7 +17,11 @@
  *   oracle_quant_channel: kernels/quant/per_channel.py:136-201 (axis -2),
  *                         :202-267 (axis -1), one-pass :35-102
  *   oracle_quant_tensor:  impls/triton_per_tensor.py:40-44 +
- *                         kernels/quant/per_tensor.py:36-43
+ *                         kernels/quant/per_tensor.py:36-43, and with
+ *                         scale_dt = the input dtype the legacy
+ *                         kernels/fp8_bmm/fp8_warper.py:21-25 +
+ *                         kernel/fp8_quant_kernel.py:56-60
+ *   oracle_round_dt:      the bf16 / fp16 rounding of torch's 0-d tensor ops
  *
  * Pinning (tests/test_oracle.py): the encoders against torch's CPU cast over
  * every fp32 bit pattern with |x| <= fp8_max; scales against closed forms
@@ -61,6 +65,34 @@ static float f16_to_f32(uint16_t h) {
     return sign ? -v : v;
   }
   return bits_to_f32(sign | ((exp + 112u) << 23) | (man << 13));
+}
+
+/* binary32 -> binary16, round to nearest even (overflow to infinity). */
+static uint16_t f32_to_f16_rne(float f) {
+  uint32_t x = f32_to_bits(f);
+  uint16_t sign = (uint16_t)((x >> 16) & 0x8000u);
+  uint32_t ax = x & 0x7FFFFFFFu;
+  if (ax > 0x7F800000u) return sign | 0x7E00u;            /* NaN */
+  if (ax >= 0x477FF000u) return sign | 0x7C00u;           /* >= 65520: tie or above rounds to inf */
+  if (ax < 0x38800000u) {                                 /* below 2^-14: subnormal or zero */
+    float r = rintf(bits_to_f32(ax) * 16777216.0f);       /* units of 2^-24, exact scaling */
+    return sign | (uint16_t)r;                            /* r == 1024 is the smallest normal */
+  }
+  uint32_t r = ax + 0xFFFu + ((ax >> 13) & 1u);           /* drop 13 mantissa bits, RNE */
+  r -= 112u << 23;                                        /* rebias 127 -> 15 */
+  return sign | (uint16_t)(r >> 13);
+}
+
+/* Round a binary32 value to `dtype` (RNE) and back; identity for OR_F32. */
+float oracle_round_dt(float f, int dtype) {
+  if (dtype == OR_BF16) {
+    uint32_t u = f32_to_bits(f);
+    if ((u & 0x7FFFFFFFu) > 0x7F800000u) return f;
+    u = (u + 0x7FFFu + ((u >> 16) & 1u)) & 0xFFFF0000u;
+    return bits_to_f32(u);
+  }
+  if (dtype == OR_F16) return f16_to_f32(f32_to_f16_rne(f));
+  return f;
 }
 
 static inline float load_elem(const void *base, int dtype, int64_t off) {
@@ -211,12 +243,20 @@ int oracle_quant_channel(const void *x, int xd, int64_t batch, int64_t m, int64_
  * Per-tensor quantization (impls/triton_per_tensor.py:40-44,
  * kernels/quant/per_tensor.py:36-43): amax over everything, clamp_min(eps),
  * qs = reciprocal(s) * fp8_max, dequant = reciprocal(qs).
+ *
+ * scale_dt is the dtype the scalar scale arithmetic is carried out in. The
+ * fp8_bench path computes it in fp32 (OR_F32). The legacy
+ * kernels/fp8_bmm/fp8_warper.py:21-25 does the same torch ops on 0-d tensors
+ * of the input's dtype, so for a bf16 / fp16 input every step rounds to that
+ * dtype: s = max(amax, dt(eps)), r = dt(1 / s), qs = dt(r * fp8_max),
+ * dequant = dt(1 / qs) (each op evaluated in fp32, as torch's opmath does,
+ * then rounded). The quantization multiplies x (as fp32) by that qs.
  */
 int oracle_quant_tensor(const void *x, int xd, int64_t batch, int64_t m, int64_t n,
                         int64_t sxb, int64_t sxm, int64_t sxn, uint8_t *y,
                         int yfmt, int64_t syb, int64_t sym, int64_t syn,
                         float *scale, float *quant_scale, float fp8_max,
-                        float eps) {
+                        float eps, int scale_dt) {
   float amax = 0.0f;
   for (int64_t b = 0; b < batch; ++b)
     for (int64_t r = 0; r < m; ++r)
@@ -224,12 +264,12 @@ int oracle_quant_tensor(const void *x, int xd, int64_t batch, int64_t m, int64_t
         float a = fabsf(load_elem(x, xd, b * sxb + r * sxm + c * sxn));
         amax = fmaxf(amax, a);
       }
-  float safe = fmaxf(amax, eps);
+  float safe = oracle_round_dt(fmaxf(oracle_round_dt(amax, scale_dt), oracle_round_dt(eps, scale_dt)), scale_dt);
   /* `fp8_max / max_abs` with a Python-float numerator is evaluated by torch
    * as max_abs.reciprocal() * fp8_max (torch/_tensor.py __rdiv__): two
    * roundings, unlike the true division of the Triton kernels. */
-  float qs = (1.0f / safe) * fp8_max;
-  float ds = 1.0f / qs; /* quant_scale.reciprocal() */
+  float qs = oracle_round_dt(oracle_round_dt(1.0f / safe, scale_dt) * fp8_max, scale_dt);
+  float ds = oracle_round_dt(1.0f / qs, scale_dt); /* quant_scale.reciprocal() */
   *scale = ds;
   if (quant_scale) *quant_scale = qs;
   for (int64_t b = 0; b < batch; ++b)

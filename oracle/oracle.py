@@ -74,7 +74,9 @@ def lib() -> ctypes.CDLL:
         L.oracle_quant_tensor.restype = ctypes.c_int
         L.oracle_quant_tensor.argtypes = (
             [_ptr, ctypes.c_int] + [_i64] * 6 + [_ptr, ctypes.c_int] + [_i64] * 3
-            + [_ptr, _ptr, ctypes.c_float, ctypes.c_float])
+            + [_ptr, _ptr, ctypes.c_float, ctypes.c_float, ctypes.c_int])
+        L.oracle_round_dt.restype = ctypes.c_float
+        L.oracle_round_dt.argtypes = [ctypes.c_float, ctypes.c_int]
         _LIB = L
     return _LIB
 
@@ -200,19 +202,33 @@ def quant_channel(x, channel_axis: int = -1, fmt="e4m3", eps: float = 1e-12,
     return q, s
 
 
-def quant_tensor(x, fmt="e4m3", eps: float = 1e-12, dtype: Optional[str] = None):
-    """Per-tensor quantization; returns (q, dequant_scale, quant_scale)."""
+def quant_tensor(x, fmt="e4m3", eps: float = 1e-12, dtype: Optional[str] = None,
+                 scale_dt: Optional[int] = None, fp8_max: Optional[float] = None):
+    """Per-tensor quantization; returns (q, dequant_scale, quant_scale).
+
+    scale_dt (F32 / BF16 / F16) is the dtype of the scale arithmetic: F32 for
+    impls/triton_per_tensor.py, the input's dtype for the legacy
+    kernels/fp8_bmm/fp8_warper.py:21-25 (pass ``scale_dt="input"``).
+    fp8_max defaults to the format's largest finite value (the legacy API's
+    fp8_range argument can override it).
+    """
     arr, xd = as_bits(x, dtype)
     b, m, n, sxb, sxm, sxn = _dims(arr)
     code = fmt_code(fmt)
+    sdt = xd if scale_dt == "input" else (F32 if scale_dt is None else scale_dt)
     q = np.empty((b, m, n), dtype=np.uint8)
     ds = np.zeros(1, dtype=np.float32)
     qs = np.zeros(1, dtype=np.float32)
     lib().oracle_quant_tensor(arr.ctypes.data, xd, b, m, n, sxb, sxm, sxn,
                               q.ctypes.data, code, m * n, n, 1, ds.ctypes.data,
-                              qs.ctypes.data, FP8_MAX[code], eps)
+                              qs.ctypes.data, FP8_MAX[code] if fp8_max is None else fp8_max, eps, sdt)
     q = q[0] if arr.ndim == 2 else q
     return q, ds[0], qs[0]
+
+
+def round_dt(v: float, dtype: int) -> float:
+    """oracle_round_dt: RNE of an fp32 value to bf16 / fp16 (identity for F32)."""
+    return float(lib().oracle_round_dt(ctypes.c_float(v), dtype))
 
 
 # ---------------------------------------------------------------------------

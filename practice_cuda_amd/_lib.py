@@ -60,7 +60,7 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.pcamd_quant_channel.restype = _int
     lib.pcamd_quant_channel.argtypes = quant_head + [_ptr, _i64, _i64, _int, _flt, _flt, _ptr]
     lib.pcamd_quant_tensor.restype = _int
-    lib.pcamd_quant_tensor.argtypes = quant_head + [_ptr, _ptr, _flt, _flt, _ptr]
+    lib.pcamd_quant_tensor.argtypes = quant_head + [_ptr, _ptr, _flt, _flt, _int, _ptr]
     lib.pcamd_bmm_scaled.restype = _int
     lib.pcamd_bmm_scaled.argtypes = (
         [_ptr, _ptr, _int] + [_i64] * 4 + [_i64] * 6 + [_ptr, _int] + [_i64] * 3

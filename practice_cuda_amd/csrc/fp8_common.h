@@ -216,12 +216,27 @@ PCAMD_DEV Scales channel_scales(float amax, float fp8_max, float eps) {
   float s = fmaxf(amax, eps);
   return {fp8_max / s, s / fp8_max};
 }
+// Round an fp32 value to dtype dt (RNE) and back; identity for kF32.
+PCAMD_DEV float round_dt(float v, int dt) {
+  if (dt == kBF16) {
+    uint32_t u = __float_as_uint(v);
+    if ((u & 0x7FFFFFFFu) > 0x7F800000u) return v;
+    return __uint_as_float((u + 0x7FFFu + ((u >> 16) & 1u)) & 0xFFFF0000u);
+  }
+  if (dt == kF16) return static_cast<float>(static_cast<_Float16>(v));
+  return v;
+}
+
 // per-tensor: the reference evaluates `fp8_max / max_abs` as a torch tensor
 // op, i.e. reciprocal(max_abs) * fp8_max (two roundings), then reciprocal.
-PCAMD_DEV Scales tensor_scales(float amax, float fp8_max, float eps) {
-  float s = fmaxf(amax, eps);
-  float qs = (1.0f / s) * fp8_max;
-  return {qs, 1.0f / qs};
+// scale_dt is the dtype those 0-d tensor ops run in: fp32 for
+// fp8_bench/impls/triton_per_tensor.py:40-44, the input's dtype for the
+// legacy kernels/fp8_bmm/fp8_warper.py:21-25 (each op evaluated in fp32, then
+// rounded to that dtype).
+PCAMD_DEV Scales tensor_scales(float amax, float fp8_max, float eps, int scale_dt = kF32) {
+  const float s = round_dt(fmaxf(round_dt(amax, scale_dt), round_dt(eps, scale_dt)), scale_dt);
+  const float qs = round_dt(round_dt(1.0f / s, scale_dt) * fp8_max, scale_dt);
+  return {qs, round_dt(1.0f / qs, scale_dt)};
 }
 
 }  // namespace pcamd

@@ -491,6 +491,7 @@ struct TensorArgs {
   int64_t sxb, sxm, sxn, syb, sym, syn;
   int64_t total;       // batch * m * n
   float fp8_max, eps;
+  int scale_dt;        // dtype of the scalar scale arithmetic (kF32 / kBF16 / kF16)
 };
 
 template <int DT>
@@ -512,7 +513,7 @@ __global__ __launch_bounds__(kThreads) void tensor_amax_kernel(TensorArgs a) {
 template <int DT, int FMT>
 __global__ __launch_bounds__(kThreads) void tensor_quant_kernel(TensorArgs a) {
   const float amax = __uint_as_float(*reinterpret_cast<const uint32_t*>(a.scale));
-  const Scales s = tensor_scales(amax, a.fp8_max, a.eps);
+  const Scales s = tensor_scales(amax, a.fp8_max, a.eps, a.scale_dt);
   const int64_t stride = static_cast<int64_t>(gridDim.x) * kThreads;
   for (int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x; i < a.total; i += stride) {
     const int64_t b = i / (a.m * a.n);
@@ -525,7 +526,7 @@ __global__ __launch_bounds__(kThreads) void tensor_quant_kernel(TensorArgs a) {
 
 __global__ void tensor_finalize_kernel(TensorArgs a) {
   const float amax = __uint_as_float(*reinterpret_cast<const uint32_t*>(a.scale));
-  const Scales s = tensor_scales(amax, a.fp8_max, a.eps);
+  const Scales s = tensor_scales(amax, a.fp8_max, a.eps, a.scale_dt);
   *a.scale = s.ds;
   if (a.quant_scale) *a.quant_scale = s.qs;
 }
@@ -907,17 +908,20 @@ extern "C" int pcamd_quant_channel(const void* x, int x_dtype, int64_t batch, in
 extern "C" int pcamd_quant_tensor(const void* x, int x_dtype, int64_t batch, int64_t m, int64_t n,
                                   int64_t sxb, int64_t sxm, int64_t sxn, void* y, int y_dtype,
                                   int64_t syb, int64_t sym, int64_t syn, float* scale,
-                                  float* quant_scale_out, float fp8_max, float eps, void* stream) {
+                                  float* quant_scale_out, float fp8_max, float eps, int scale_dtype,
+                                  void* stream) {
   clear_error();
   int rc = validate_common(x, x_dtype, batch, m, n, y, y_dtype, scale, fp8_max);
   if (rc) return rc;
   if (!scale) return set_error(PCAMD_ERR_INVALID, "null scale pointer");
+  if (scale_dtype != kF32 && scale_dtype != kBF16 && scale_dtype != kF16)
+    return set_error(PCAMD_ERR_INVALID, "scale_dtype must be f32, bf16 or f16 (got %d)", scale_dtype);
   TensorArgs a{};
   a.x = static_cast<const char*>(x); a.y = static_cast<uint8_t*>(y); a.scale = scale;
   a.quant_scale = quant_scale_out;
   a.batch = batch; a.m = m; a.n = n; a.sxb = sxb; a.sxm = sxm; a.sxn = sxn;
   a.syb = syb; a.sym = sym; a.syn = syn; a.total = batch * m * n;
-  a.fp8_max = fp8_max; a.eps = eps;
+  a.fp8_max = fp8_max; a.eps = eps; a.scale_dt = scale_dtype;
   return dispatch_dt_fmt<LaunchTensor>(x_dtype, y_dtype, a, static_cast<hipStream_t>(stream));
 }
 

@@ -18,18 +18,26 @@ from ..registry import QuantResult, register_bmm, register_quant
 from . import _common as C
 
 
-def quant_tensor_raw(x: torch.Tensor, fp8_dtype: torch.dtype, eps: float):
-    """Launch the per-tensor kernels; returns (fp8 tensor, dequant scale, quant scale)."""
+def quant_tensor_raw(x: torch.Tensor, fp8_dtype: torch.dtype, eps: float, *,
+                     fp8_max: float | None = None, scale_dtype: torch.dtype = torch.float32):
+    """Launch the per-tensor kernels; returns (fp8 tensor, dequant scale, quant scale).
+
+    scale_dtype is the dtype the scalar scale steps are rounded to (fp32 for
+    the fp8_bench path; the input's dtype for the legacy fp8_warper API).
+    fp8_max defaults to the fp8 format's largest finite value.
+    """
     output = torch.empty_like(x, dtype=fp8_dtype, memory_format=torch.preserve_format)
     batch, m, n, xs, ys = C.dims3(x, output)
     scales = torch.empty(2, device=x.device, dtype=torch.float32)
     L = _lib.lib()
+    _lib.require_gpu_tensor(x, "x")
     with torch.cuda.device(x.device):
         rc = L.pcamd_quant_tensor(
             _lib.ptr(x), _lib.dtype_code(x.dtype), batch, m, n, *xs,
             _lib.ptr(output), _lib.dtype_code(fp8_dtype), *ys,
             _lib.ptr(scales[0:1]), _lib.ptr(scales[1:2]),
-            float(torch.finfo(fp8_dtype).max), float(eps), _lib.stream_of(x))
+            float(torch.finfo(fp8_dtype).max if fp8_max is None else fp8_max), float(eps),
+            _lib.dtype_code(scale_dtype), _lib.stream_of(x))
     _lib.check(rc, "pcamd_quant_tensor")
     return output, scales[0], scales[1]
 
