@@ -236,9 +236,40 @@ def bench_config5(torch, steps, warmup, dev):
         res[name] = {"ms": ms, "TFLOP/s": t, "frac_of_fp8_peak": t / FP8_PEAK_TFLOPS}
     total_ms = sum(r["ms"] for r in res.values())
     tflops = 3 * flops / (total_ms * 1e-3) / 1e12
+    layer = layer_step(torch, X, W, dY, steps, dev)
+    layer["TFLOP/s"] = 3 * flops / (layer["ms"] * 1e-3) / 1e12
     return {"name": "config5_training_linear_m8192_k4096_n14336", "ms_per_step": total_ms,
             "value": tflops, "unit": "TFLOP/s", "frac_of_fp8_peak": tflops / FP8_PEAK_TFLOPS,
-            "gemms": res, "flops_per_step": 3 * flops}
+            "gemms": res, "flops_per_step": 3 * flops, "layer_step": layer}
+
+
+def layer_step(torch, X, W, dY, steps, dev):
+    """Forward + backward of Float8BMMLinear at the config-5 shape: the five
+    fp8 quantization passes (X 1x128, W 128x128, dY 1x128, dY and X 128x1)
+    and the three GEMMs, eager (autograd), timed with events."""
+    from practice_cuda_amd.modules import Float8BMMLinear
+    layer = Float8BMMLinear(1, X.shape[1], W.shape[0], bias=False, device=dev, dtype=torch.bfloat16)
+    with torch.no_grad():
+        layer.weight.copy_(W[None])
+    xg = X[None].detach().requires_grad_(True)
+    dy = dY[None]
+
+    def step():
+        layer.weight.grad = None
+        xg.grad = None
+        layer(xg).backward(dy)
+
+    for _ in range(2):
+        step()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(steps):
+        step()
+    end.record()
+    torch.cuda.synchronize()
+    return {"ms": start.elapsed_time(end) / steps,
+            "what": "Float8BMMLinear forward + backward, 5 quantization passes + 3 GEMMs, eager"}
 
 
 # ---------------------------------------------------------------------------
