@@ -526,7 +526,7 @@ extern "C" int pcamd_bmm_scaled(const void* a, const void* b, int ab_dtype, int6
       const int fmode = scale_mode == PCAMD_SCALE_BLOCK ? 0 : scale_mode == PCAMD_SCALE_CHANNEL ? 1 : 2;
       const bool sb_col = scale_mode == PCAMD_SCALE_BLOCK && args.qbn < 16;
       const bool qb1 = scale_mode == PCAMD_SCALE_BLOCK && args.qbk == 128;
-      if (wide) return bmm_wide_launch(f, ab_dtype, a_k, b_k, fmode, sb_col, st);
+      if (wide) return bmm_wide_launch(f, ab_dtype, a_k, b_k, fmode, st);
       return bmm_fast_launch(f, ab_dtype, a_k, b_k, fmode, sb_col, qb1, st);
     }
   }

@@ -35,9 +35,8 @@ int bmm_fast_tile_m();
 int bmm_fast_tile_n();
 
 // 256 x 256-tile, 8-wave kernel for two or more K steps (bmm_wide.hip)
-// block mode requires quant_block_k == 128
-int bmm_wide_launch(const FastArgs& a, int ab_dtype, bool a_k, bool b_k, int mode, bool sb_col,
-                    hipStream_t st);
+// block mode requires quant_block_k == 128 and power-of-two qbm / qbn
+int bmm_wide_launch(const FastArgs& a, int ab_dtype, bool a_k, bool b_k, int mode, hipStream_t st);
 int bmm_wide_tile();
 
 }  // namespace pcamd

@@ -62,6 +62,9 @@ constexpr uint32_t kRsrcWord3 = 0x00020000u;
 // consecutive ones but (among the groupings that fit) eight rows of two
 // adjacent g. swz_k = 5 * bit1(r) ^ bit2(r) spreads the 16 (row, chunk) pairs
 // of each such group over distinct bank groups for all of them.
+template <int N>
+using IC = std::integral_constant<int, N>;
+
 PCAMD_DEV int swz_k(int r) { return (((r >> 1) & 1) * 5) ^ ((r >> 2) & 1); }
 // MN-major tile (256-byte k-rows): chunk c of k-row k sits at position
 // c ^ (k & 7) ^ (8 ((k >> 5) & 1)). A 16-lane group reads 8 k-rows k0..k0+7
@@ -197,6 +200,31 @@ PCAMD_DEV v4f mfma(const v8i& x, const v8i& y, const v4f& c) {
   return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(x, y, c, code, code, 0, 0, 0, 0);
 }
 
+// Block-mode step for one row block: p_new = A x B (fresh 16x16 partial), then
+// acc += p_old * f (the partial of the previous sub-tile, produced four MFMAs
+// earlier). One asm block fixes that order: scheduled as separate
+// instructions, each fold is hoisted next to the MFMA that produces its input
+// and the wave stalls on the result. f[r] is the factor of output r (the same
+// value four times when it only depends on the row). p_old was written at
+// least three MFMAs and twelve VALU instructions earlier, more than the
+// XDL-write -> VALU-read wait states of an 8-pass MFMA.
+template <int FMT>
+PCAMD_DEV void mfma_fold(const v8i& x, const v8i& y, v4f& p_new, const v4f& p_old, float& a0, float& a1, float& a2,
+                         float& a3, float f0, float f1, float f2, float f3) {
+#define PCAMD_MFMA_FOLD(MOD)                                                                   \
+  asm volatile("v_mfma_f32_16x16x128_f8f6f4 %0, %5, %6, 0" MOD "\n\t"                          \
+               "v_fmac_f32_e32 %1, %7, %11\n\t"                                                 \
+               "v_fmac_f32_e32 %2, %8, %12\n\t"                                                 \
+               "v_fmac_f32_e32 %3, %9, %13\n\t"                                                 \
+               "v_fmac_f32_e32 %4, %10, %14"                                                    \
+               : "=&v"(p_new), "+v"(a0), "+v"(a1), "+v"(a2), "+v"(a3)                           \
+               : "v"(x), "v"(y), "v"(p_old[0]), "v"(p_old[1]), "v"(p_old[2]), "v"(p_old[3]),   \
+                 "v"(f0), "v"(f1), "v"(f2), "v"(f3))
+  if constexpr (FMT == kE5M2) PCAMD_MFMA_FOLD(" cbsz:1 blgp:1");
+  else PCAMD_MFMA_FOLD("");
+#undef PCAMD_MFMA_FOLD
+}
+
 PCAMD_DEV uint32_t pack_bf16x2(float lo, float hi) {
   return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<__bf16>(lo))) |
          (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<__bf16>(hi))) << 16);
@@ -231,13 +259,26 @@ __device__ __attribute__((noinline)) void epilogue_general(void* c, int64_t c_ro
   }
 }
 
-// MODE: 0 block (qbk == 128), 1 channel, 2 tensor. SB_COL: block scales with
-// qbn < 16 (one B scale per output column).
+// MODE: 0 block (qbk == 128), 1 channel, 2 tensor. SBK (block mode): how
+// the B scales vary over a wave's 128 columns - 0: one scale (qbn >= 128),
+// 1: one per 16-column sub-tile (16 <= qbn < 128), 2: one per column.
 //
 // Block scales are staged through LDS one K step ahead (sa for the tile's
 // 256 rows, sb for its 256 columns), so the fold acc += P * (sa * sb) reads
 // them with a few ds_reads instead of holding them in registers.
-template <bool A_K, bool B_K, int FMT, int MODE, bool SB_COL>
+//
+// Schedule of one K step (8 sub-tiles j of 4 MFMAs each, one per row block i):
+//   - the B fragment of sub-tile j + 1 is read while sub-tile j issues;
+//   - block mode: the MFMA (i, j) writes a fresh partial p[i]; just before it,
+//     the previous partial p[i] (sub-tile j - 1, or sub-tile 7 of the previous
+//     step) is folded, acc += p * factor, so the 4 fold FMAs of each MFMA run
+//     in the matrix core's shadow and one set of partials is live;
+//   - the step boundary sits in front of sub-tile 7: wait for the next
+//     stage's DMA, barrier, start the DMA two steps ahead, read the next
+//     step's first B fragment; the next step's A fragment i is read right
+//     after MFMA (i, 7) has consumed the current one. The last sub-tile's
+//     MFMAs cover the latency of those reads.
+template <bool A_K, bool B_K, int FMT, int MODE, int SBK>
 __global__ __launch_bounds__(NT, 1) void bmm_wide_kernel(FastArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   float* sa_tile = reinterpret_cast<float*>(smem + 2 * STAGE);  // [2][BM]
@@ -303,69 +344,170 @@ __global__ __launch_bounds__(NT, 1) void bmm_wide_kernel(FastArgs a) {
 #pragma unroll
     for (int j = 0; j < 8; ++j) acc[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
 
-  // one K step on the stage of step ks
-  auto compute = [&](int ks) {
-    const uint8_t* cur = smem + (ks & 1) * STAGE;
-    v8i af[4];
+  const int ksteps = a.k / BK;  // >= 2
+  // prologue: step 0 resident in stage 0, step 1 in flight to stage 1
+  issue(0, smem);
+  if constexpr (MODE == 0) store_scale(0, load_scale(0));
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  issue(1, smem + STAGE);
+  float sc_next = 0.0f;
+  if constexpr (MODE == 0) sc_next = load_scale(1);
+
+  v8i af[4], bf[2];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) af[i] = afrag(cur, i);
-    if constexpr (MODE != 0) {
+  for (int i = 0; i < 4; ++i) af[i] = afrag(smem, i);
+  bf[0] = bfrag(smem, 0);
+
+  // Block-mode fold state. The factor of output (i, r) of a sub-tile is the
+  // row factor f[i] (sa * sb for SBK 0 / 1, sa for SBK 2) times, for SBK 2,
+  // the column scale c[r]. p / pf / pc: the pending partials and their
+  // factors. Row scales of a step: sa_c (fc = sa_c * sb for SBK 0); column
+  // scales of sub-tile j (SBK 1 / 2): cs[j & 1], read one sub-tile ahead.
+  v4f p[4];
+  float pf[4], pc[4], sa_c[4], fc[4];
+  float4 cs[2];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const v8i bf = bfrag(cur, j);
+  for (int i = 0; i < 4; ++i) {
+    p[i] = v4f{0.f, 0.f, 0.f, 0.f};
+    pf[i] = pc[i] = sa_c[i] = fc[i] = 0.0f;
+  }
+  cs[0] = cs[1] = float4{0.f, 0.f, 0.f, 0.f};
+  const int sa_off = wm * 64 + lr;
+  const int sb_off = wn * 128 + (SBK == 2 ? 4 * lg : 0);
+  auto read_rows = [&](int ks, float (&sa)[4], float (&f)[4]) {
+    const float* sat = sa_tile + (ks & 1) * BM + sa_off;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) acc[i][j] = mfma<FMT>(bf, af[i], acc[i][j]);
-      }
-    } else {
-      const float* sat = sa_tile + (ks & 1) * BM + wm * 64 + lr;
-      const float* sbt = sb_tile + (ks & 1) * BN + wn * 128 + 4 * lg;
-      float sav[4];
+    for (int i = 0; i < 4; ++i) sa[i] = sat[16 * i];
+    if constexpr (SBK == 0) {
+      const float sb = sb_tile[(ks & 1) * BN + sb_off];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) sav[i] = sat[16 * i];
-      // acc[.][j] += P_j * (sa * sb): the MFMAs of sub-tile j are issued, then
-      // sub-tile j - 1 is folded while they run, so only two sub-tiles of
-      // partials are live at a time.
-      auto fold = [&](int j, const v4f (&p)[4]) {
-        float sb4[4];
-        if constexpr (SB_COL) {
-          const float4 v = *reinterpret_cast<const float4*>(sbt + 16 * j);
-          sb4[0] = v.x; sb4[1] = v.y; sb4[2] = v.z; sb4[3] = v.w;
-        } else {
-          sb4[0] = sbt[16 * j];
+      for (int i = 0; i < 4; ++i) f[i] = sa[i] * sb;
+    }
+  };
+  auto read_cols = [&](int ks, int j) {
+    const float* sbt = sb_tile + (ks & 1) * BN + sb_off + 16 * j;
+    if constexpr (SBK == 1) cs[j & 1].x = sbt[0];
+    if constexpr (SBK == 2) cs[j & 1] = *reinterpret_cast<const float4*>(sbt);
+  };
+  if constexpr (MODE == 0) {
+    read_rows(0, sa_c, fc);
+    read_cols(0, 0);
+  }
+
+  using T = std::true_type;
+  using F = std::false_type;
+  // MFMAs of sub-tile j (B fragment bcur), each preceded by the fold of the
+  // pending partial of its row block (sub-tile j - 1, or 7 of the previous
+  // step); with af_next, the next step's A fragment i is read right after
+  // MFMA (i, j). ds_reads: LDS reads issued in the same scheduling region
+  // ahead of the MFMAs (the next B fragment and scales).
+  auto subtile = [&](int j, const v8i& bcur, const uint8_t* af_next, auto ds_reads_c, auto next_c) {
+    constexpr int ds_reads = decltype(ds_reads_c)::value;
+    constexpr bool NEXT = decltype(next_c)::value;
+    const int jp = (j + 7) & 7;
+    float cf[4], cc[4];
+    if constexpr (MODE == 0) {
+      const float4 c = cs[j & 1];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) cf[i] = SBK == 0 ? fc[i] : SBK == 1 ? sa_c[i] * c.x : sa_c[i];
+      cc[0] = c.x; cc[1] = c.y; cc[2] = c.z; cc[3] = c.w;
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      if constexpr (MODE == 0) {
+        float f[4], a[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          f[r] = SBK == 2 ? pf[i] * pc[r] : pf[i];
+          a[r] = acc[i][jp][r];
         }
+        v4f pn;
+        mfma_fold<FMT>(bcur, af[i], pn, p[i], a[0], a[1], a[2], a[3], f[0], f[1], f[2], f[3]);
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-#pragma unroll
-          for (int r = 0; r < 4; ++r) acc[i][j][r] += p[i][r] * (sav[i] * sb4[SB_COL ? r : 0]);
-      };
-      v4f p[2][4];
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const v8i bf = bfrag(cur, j);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) p[j & 1][i] = mfma<FMT>(bf, af[i], v4f{0.f, 0.f, 0.f, 0.f});
-        if (j > 0) fold(j - 1, p[(j - 1) & 1]);
-        __builtin_amdgcn_sched_barrier(0);
+        for (int r = 0; r < 4; ++r) acc[i][jp][r] = a[r];
+        p[i] = pn;
+      } else {
+        acc[i][j] = mfma<FMT>(bcur, af[i], acc[i][j]);
       }
-      fold(7, p[1]);
+      if constexpr (NEXT) af[i] = afrag(af_next, i);
+    }
+    if constexpr (MODE == 0) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        pf[i] = cf[i];
+        pc[i] = cc[i];
+      }
+    }
+    // Instruction order of the sub-tile (sched_group_barrier: mask, count,
+    // pipeline id; masks 0x2 VALU, 0x8 MFMA, 0x100 DS read): its LDS reads
+    // first, then per row block the fold VALU followed by the MFMA, and with
+    // af_next the A fragment read behind each MFMA. Pure arithmetic carries no
+    // ordering of its own, and without this the folds sink below all MFMAs.
+    if constexpr (MODE != 0) {
+      if constexpr (ds_reads > 0) __builtin_amdgcn_sched_group_barrier(0x100, ds_reads, 0);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        if constexpr (NEXT) __builtin_amdgcn_sched_group_barrier(0x100, A_K ? 2 : 4, 0);
+      }
     }
   };
 
-  const int ksteps = a.k / BK;  // >= 2
-  issue(0, smem);
-  if constexpr (MODE == 0) store_scale(0, load_scale(0));
-  for (int ks = 0; ks < ksteps - 1; ++ks) {
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
-    float next_scale = 0.0f;
-    if constexpr (MODE == 0) next_scale = load_scale(ks + 1);
-    issue(ks + 1, smem + ((ks + 1) & 1) * STAGE);
-    compute(ks);
-    if constexpr (MODE == 0) store_scale(ks + 1, next_scale);
+  // One K step. BOUNDARY: the next step follows (barrier and fragment
+  // reads in front of sub-tile 7); DMA: also start the DMA two steps ahead.
+  // Both are compile-time so that the main loop body is one basic block:
+  // with a branch at the step boundary the compiler sinks the folds of the
+  // earlier sub-tiles past it and keeps all their partials live.
+  constexpr int kBReads = B_K ? 2 : 4;  // ds_read instructions per B fragment
+  auto step = [&](int ks, auto boundary, auto dma) {
+    constexpr bool BOUNDARY = decltype(boundary)::value;
+    constexpr bool DMA = decltype(dma)::value;
+    const uint8_t* cur = smem + (ks & 1) * STAGE;
+    const uint8_t* nxt = smem + ((ks + 1) & 1) * STAGE;
+#pragma unroll
+    for (int j = 0; j < 7; ++j) {
+      const v8i bcur = bf[j & 1];
+      bf[(j + 1) & 1] = bfrag(cur, j + 1);
+      if constexpr (MODE == 0 && SBK != 0) read_cols(ks, j + 1);
+      subtile(j, bcur, nullptr, IC<kBReads + (MODE == 0 && SBK != 0 ? 1 : 0)>{}, F{});
+    }
+    if constexpr (BOUNDARY) {
+      if constexpr (MODE == 0) store_scale(ks + 1, sc_next);
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      __syncthreads();
+      if constexpr (DMA) {
+        issue(ks + 2, const_cast<uint8_t*>(cur));
+        if constexpr (MODE == 0) sc_next = load_scale(ks + 2);
+      }
+      bf[0] = bfrag(nxt, 0);
+      if constexpr (MODE == 0) {
+        // cs[1] (sub-tile 7) is still needed; cs[0] takes sub-tile 0 of the next step
+        if constexpr (SBK != 0) read_cols(ks + 1, 0);
+        float sa_n[4], fc_n[4];
+        read_rows(ks + 1, sa_n, fc_n);
+        subtile(7, bf[1], nxt, IC<kBReads + (SBK != 0 ? 1 : 0) + (SBK == 0 ? 3 : 2)>{}, T{});
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          sa_c[i] = sa_n[i];
+          fc[i] = fc_n[i];
+        }
+      } else {
+        subtile(7, bf[1], nxt, IC<kBReads>{}, T{});
+      }
+    } else {
+      subtile(7, bf[1], nullptr, IC<0>{}, F{});
+    }
+  };
+  for (int ks = 0; ks < ksteps - 2; ++ks) step(ks, T{}, T{});
+  step(ksteps - 2, T{}, F{});
+  step(ksteps - 1, F{}, F{});
+  if constexpr (MODE == 0) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) acc[i][7][r] += p[i][r] * (SBK == 2 ? pf[i] * pc[r] : pf[i]);
   }
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  __syncthreads();
-  compute(ksteps - 1);
 
   const int row_base = m0 + wm * 64 + lr;
   const int col_base = n0 + wn * 128 + 4 * lg;
@@ -446,9 +588,9 @@ __global__ __launch_bounds__(NT, 1) void bmm_wide_kernel(FastArgs a) {
 
 constexpr int LDS_BYTES = 2 * STAGE + 2 * (BM + BN) * 4;
 
-template <bool A_K, bool B_K, int FMT, int MODE, bool SB_COL>
+template <bool A_K, bool B_K, int FMT, int MODE, int SBK>
 int launch_one(const FastArgs& a, hipStream_t st) {
-  auto kern = bmm_wide_kernel<A_K, B_K, FMT, MODE, SB_COL>;
+  auto kern = bmm_wide_kernel<A_K, B_K, FMT, MODE, SBK>;
   static bool configured = false;  // benign race: the attribute call is idempotent
   if (!configured) {
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
@@ -460,27 +602,30 @@ int launch_one(const FastArgs& a, hipStream_t st) {
   return check_launch("bmm_wide_kernel");
 }
 
+// block mode: B-scale kind from the quant block width (qbn = 1 << qbn_shift):
+// >= 128 one scale per wave, >= 16 one per 16-column sub-tile, else per column
 template <bool A_K, bool B_K, int FMT>
-int launch_mode(const FastArgs& a, int mode, bool sb_col, hipStream_t st) {
-  if (mode == 1) return launch_one<A_K, B_K, FMT, 1, false>(a, st);
-  if (mode == 2) return launch_one<A_K, B_K, FMT, 2, false>(a, st);
-  return sb_col ? launch_one<A_K, B_K, FMT, 0, true>(a, st) : launch_one<A_K, B_K, FMT, 0, false>(a, st);
+int launch_mode(const FastArgs& a, int mode, hipStream_t st) {
+  if (mode == 1) return launch_one<A_K, B_K, FMT, 1, 0>(a, st);
+  if (mode == 2) return launch_one<A_K, B_K, FMT, 2, 0>(a, st);
+  if (a.qbn_shift >= 7) return launch_one<A_K, B_K, FMT, 0, 0>(a, st);
+  if (a.qbn_shift >= 4) return launch_one<A_K, B_K, FMT, 0, 1>(a, st);
+  return launch_one<A_K, B_K, FMT, 0, 2>(a, st);
 }
 
 template <int FMT>
-int launch_layout(const FastArgs& a, bool a_k, bool b_k, int mode, bool sb_col, hipStream_t st) {
-  if (a_k && b_k) return launch_mode<true, true, FMT>(a, mode, sb_col, st);
-  if (a_k) return launch_mode<true, false, FMT>(a, mode, sb_col, st);
-  if (b_k) return launch_mode<false, true, FMT>(a, mode, sb_col, st);
-  return launch_mode<false, false, FMT>(a, mode, sb_col, st);
+int launch_layout(const FastArgs& a, bool a_k, bool b_k, int mode, hipStream_t st) {
+  if (a_k && b_k) return launch_mode<true, true, FMT>(a, mode, st);
+  if (a_k) return launch_mode<true, false, FMT>(a, mode, st);
+  if (b_k) return launch_mode<false, true, FMT>(a, mode, st);
+  return launch_mode<false, false, FMT>(a, mode, st);
 }
 
 }  // namespace bmmw
 
-int bmm_wide_launch(const FastArgs& a, int ab_dtype, bool a_k, bool b_k, int mode, bool sb_col,
-                    hipStream_t st) {
-  if (ab_dtype == kE5M2) return bmmw::launch_layout<kE5M2>(a, a_k, b_k, mode, sb_col, st);
-  return bmmw::launch_layout<kE4M3>(a, a_k, b_k, mode, sb_col, st);
+int bmm_wide_launch(const FastArgs& a, int ab_dtype, bool a_k, bool b_k, int mode, hipStream_t st) {
+  if (ab_dtype == kE5M2) return bmmw::launch_layout<kE5M2>(a, a_k, b_k, mode, st);
+  return bmmw::launch_layout<kE4M3>(a, a_k, b_k, mode, st);
 }
 
 int bmm_wide_tile() { return bmmw::BM; }

@@ -104,6 +104,22 @@ def test_bmm_multi_block_quant_k(dev):
     assert O.max_abs_rel(out.float().cpu().numpy(), ref) <= TOL
 
 
+@pytest.mark.parametrize("qbn", [1, 8, 16, 32, 64, 128, 256])
+@pytest.mark.parametrize("b_layout", ["n", "k"])
+def test_bmm_b_block_widths(dev, qbn, b_layout):
+    # B quant blocks of every width class of the 256x256-tile kernel: one scale
+    # per column (< 16), per 16-column sub-tile (16..64), per wave (>= 128);
+    # K = 640 gives five K steps, shapes span several output tiles
+    print(f"bmm b-block width {qbn} layout {b_layout}", flush=True)
+    a, b = rand((2, 300, 640), 10), rand((2, 640, 520), 11)
+    qa = hip_per_block_quant(a.to(dev), block_m=1, block_n=128)
+    b_in = materialize(b, "k_of_b") if b_layout == "k" else b
+    qb = hip_per_block_quant(b_in.to(dev), block_m=128, block_n=qbn)
+    out = hip_per_block_bmm(qa, qb)
+    ref = O.bmm_reference(qa.dequantize().double().cpu().numpy(), qb.dequantize().double().cpu().numpy())
+    assert O.max_abs_rel(out.float().cpu().numpy(), ref) <= TOL
+
+
 def test_bmm_golden(dev):
     import os
     d = np.load(os.path.join(os.path.dirname(__file__), "golden", "bmm_golden.npz"))
