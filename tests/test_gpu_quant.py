@@ -155,6 +155,18 @@ def test_block_quant_strided_input(dev):
     assert_same(r, q_ref, s_ref, "transposed")
 
 
+@pytest.mark.parametrize("bm,bn", [(1, 128), (1, 64), (128, 128)])
+def test_block_quant_padded_rows(dev, bm, bn):
+    # rows contiguous but with a row pitch wider than the row (a column slice of
+    # a wider 3-D tensor): the row-indexed kernels, not the flat one
+    base = make_input((2, 256, 640), "bf16", seed=11).to(dev)
+    x = base[:, :, :384]
+    print(f"padded rows {bm}x{bn}", flush=True)
+    r = hip_per_block_quant(x, block_m=bm, block_n=bn)
+    q_ref, s_ref = O.quant_block(x.cpu().contiguous(), bm, bn)
+    assert_same(r, q_ref, s_ref, f"padded {bm}x{bn}")
+
+
 def test_block_quant_zeros_and_outliers(dev):
     x = torch.zeros(4, 384, device=dev, dtype=torch.bfloat16)
     x[1, 5] = -0.0
