@@ -69,4 +69,45 @@ PCAMD_DEV void store_subtile_staged(uint8_t* stg, __bf16* c, int64_t scm, int m,
   }
 }
 
+// Half-width variant: stg is 4 KiB of LDS private to this wave; the region
+// covers rows row0 .. row0 + 63 and columns col0 .. col0 + 63, and
+// value(i, jj, v) fills the 4 outputs of this lane in MFMA tile (i, jj): row
+// row0 + 16 i + (lane & 15), columns col0 + 16 jj + 4 (lane >> 4) + r. Two
+// pieces of 32 rows; staged chunk c of row r sits at LDS position c ^ (r & 7).
+// Each store instruction writes 8 rows x 128 contiguous bytes.
+template <typename ValueFn>
+PCAMD_DEV void store_half_staged(uint8_t* stg, __bf16* c, int64_t scm, int m, int n, int row0, int col0, int lane,
+                                 ValueFn&& value) {
+  typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+  const int lr = lane & 15, lg = lane >> 4;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) {
+#pragma unroll
+      for (int il = 0; il < 2; ++il) {
+        float v[4];
+        value(2 * h + il, jj, v);
+        const int r = 16 * il + lr;
+        const int chunk = 2 * jj + (lg >> 1);
+        uint2* dst = reinterpret_cast<uint2*>(stg + r * 128 + ((chunk ^ (r & 7)) << 4) + ((lg & 1) << 3));
+        *dst = make_uint2(pack_bf16_pair(v[0], v[1]), pack_bf16_pair(v[2], v[3]));
+      }
+    }
+    // LDS operations of one wave complete in order; the wait keeps the
+    // compiler from moving the reads above the writes.
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+    for (int it = 0; it < 4; ++it) {
+      const int r = 8 * it + (lane >> 3);
+      const int chunk = lane & 7;
+      const u32x4 v = *reinterpret_cast<const u32x4*>(stg + r * 128 + ((chunk ^ (r & 7)) << 4));
+      const int mm = row0 + 32 * h + r;
+      const int nn = col0 + 8 * chunk;
+      if (mm < m && nn < n) __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(c + int64_t(mm) * scm + nn));
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  }
+}
+
 }  // namespace pcamd

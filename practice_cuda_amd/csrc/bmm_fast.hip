@@ -409,10 +409,14 @@ __global__ __launch_bounds__(NT, 1) void bmm_fast_kernel(FastArgs a) {
 
 // K <= 128 (one K step, one quant-K block): a single LDS stage (48 KiB), the
 // MFMA result is scaled once in the epilogue (acc = P * sa * sb for block
-// scales), and two workgroups share a CU so one's stores overlap the other's
-// loads and MFMAs. This is the output-bound config-4 shape.
-template <bool A_K, bool B_K, int FMT, int MODE, bool SB_COL>
-__global__ __launch_bounds__(NT, 2) void bmm_single_kernel(FastArgs a) {
+// scales). This is the output-bound config-4 shape, limited by how many tiles
+// are in flight: the wave's 64 x 128 output is computed and stored in two
+// 64 x 64 halves, so three workgroups share a CU and one's stores overlap the
+// others' loads and MFMAs.
+// STAGED: plain bf16 output with aligned rows (staged_output_ok, decided on
+// the host); otherwise the direct epilogue (bias, activation, other dtypes).
+template <bool A_K, bool B_K, int FMT, int MODE, bool SB_COL, bool STAGED>
+__global__ __launch_bounds__(NT, STAGED ? 3 : 2) void bmm_single_kernel(FastArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   const int t = threadIdx.x;
   const int lane = t & 63, wave = t >> 6;
@@ -482,56 +486,63 @@ __global__ __launch_bounds__(NT, 2) void bmm_single_kernel(FastArgs a) {
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
 
-  v4f acc[4][8];
-  {
-    v8i af[4];
+  v8i af[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) af[i] = frag(smem, wm * 64 + i * 16 + lr, lg);
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const v8i bf = frag(smem + A_BYTES, wn * 128 + j * 16 + lr, lg);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) acc[i][j] = mfma<FMT>(bf, af[i], v4f{0.f, 0.f, 0.f, 0.f});
-    }
-  }
-
+  for (int i = 0; i < 4; ++i) af[i] = frag(smem, wm * 64 + i * 16 + lr, lg);
   float tscale = 1.0f;
   if constexpr (MODE == 2) tscale = a.scales_are_quant ? 1.0f / (a.sa[0] * a.sb[0]) : a.sa[0];
   const bool plain = a.bias == nullptr && a.act == PCAMD_ACT_NONE && a.c_dtype == kBF16;
-  auto value = [&](int i, int j, float (&v)[4]) {
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      float s;
-      if constexpr (MODE == 0) s = sav[i] * sbv[j][SB_COL ? r : 0];  // (sa * sb), then * P
-      else if constexpr (MODE == 1) {
-        s = sav[i] * sbv[j][r];
-        if (a.scales_are_quant) s = 1.0f / s;
-      } else s = tscale;
-      v[r] = acc[i][j][r] * s;
-    }
-  };
-  if (staged_output_ok(a.c, a.scb, a.scm, a.n, plain)) {
-    __syncthreads();  // every wave has read its fragments: the stage is free
-    store_subtile_staged(smem + wave * 8192, reinterpret_cast<__bf16*>(a.c) + bidx * a.scb, a.scm, a.m, a.n,
-                         m0 + wm * 64, n0 + wn * 128, lane, value);
-    return;
+  if constexpr (STAGED) {
+    // every wave holds its A fragments: the A region becomes the staging area
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __syncthreads();
   }
+  // The wave's 64 x 128 output in two 64 x 64 halves, so only 64
+  // accumulators are live and three workgroups fit on a CU.
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int mm = row_base + 16 * i;
+  for (int h = 0; h < 2; ++h) {
+    v4f acc[4][4];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int nn = col_base + 16 * j;
-      float v[4];
-      value(i, j, v);
-      if (mm >= a.m || nn >= a.n) continue;
-      __bf16* p = reinterpret_cast<__bf16*>(a.c) + bidx * a.scb + int64_t(mm) * a.scm + nn;
-      if (plain && nn + 4 <= a.n && (reinterpret_cast<uintptr_t>(p) & 7) == 0) {
-        *reinterpret_cast<uint2*>(p) = make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
-      } else {
-        epilogue_general(a.c, bidx * a.scb + int64_t(mm) * a.scm, a.c_dtype, a.bias,
-                         bidx * a.sbiasb + int64_t(mm) * a.sbiasm, a.sbiasn, a.bias_dtype, a.act, nn,
-                         min(4, a.n - nn), v[0], v[1], v[2], v[3]);
+    for (int jj = 0; jj < 4; ++jj) {
+      const v8i bf = frag(smem + A_BYTES, wn * 128 + (4 * h + jj) * 16 + lr, lg);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc[i][jj] = mfma<FMT>(bf, af[i], v4f{0.f, 0.f, 0.f, 0.f});
+    }
+    auto value = [&](int i, int jj, float (&v)[4]) {
+      const int j = 4 * h + jj;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        float s;
+        if constexpr (MODE == 0) s = sav[i] * sbv[j][SB_COL ? r : 0];  // (sa * sb), then * P
+        else if constexpr (MODE == 1) {
+          s = sav[i] * sbv[j][r];
+          if (a.scales_are_quant) s = 1.0f / s;
+        } else s = tscale;
+        v[r] = acc[i][jj][r] * s;
+      }
+    };
+    if constexpr (STAGED) {
+      store_half_staged(smem + wave * 4096, reinterpret_cast<__bf16*>(a.c) + bidx * a.scb, a.scm, a.m, a.n,
+                        m0 + wm * 64, n0 + wn * 128 + 64 * h, lane, value);
+      continue;
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int mm = row_base + 16 * i;
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj) {
+        const int nn = col_base + 16 * (4 * h + jj);
+        float v[4];
+        value(i, jj, v);
+        if (mm >= a.m || nn >= a.n) continue;
+        __bf16* p = reinterpret_cast<__bf16*>(a.c) + bidx * a.scb + int64_t(mm) * a.scm + nn;
+        if (plain && nn + 4 <= a.n && (reinterpret_cast<uintptr_t>(p) & 7) == 0) {
+          *reinterpret_cast<uint2*>(p) = make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
+        } else {
+          epilogue_general(a.c, bidx * a.scb + int64_t(mm) * a.scm, a.c_dtype, a.bias,
+                           bidx * a.sbiasb + int64_t(mm) * a.sbiasm, a.sbiasn, a.bias_dtype, a.act, nn,
+                           min(4, a.n - nn), v[0], v[1], v[2], v[3]);
+        }
       }
     }
   }
@@ -539,8 +550,11 @@ __global__ __launch_bounds__(NT, 2) void bmm_single_kernel(FastArgs a) {
 
 template <bool A_K, bool B_K, int FMT, int MODE, bool SB_COL>
 int launch_single(const FastArgs& a, hipStream_t st) {
-  auto kern = bmm_single_kernel<A_K, B_K, FMT, MODE, SB_COL>;
-  kern<<<a.total_tiles, NT, STAGE, st>>>(a);
+  const bool plain = a.bias == nullptr && a.act == PCAMD_ACT_NONE && a.c_dtype == kBF16;
+  const bool staged = plain && (a.n & 7) == 0 && (a.scm & 7) == 0 && (a.scb & 7) == 0 &&
+                      (reinterpret_cast<uintptr_t>(a.c) & 15) == 0;  // staged_output_ok on the host
+  if (staged) bmm_single_kernel<A_K, B_K, FMT, MODE, SB_COL, true><<<a.total_tiles, NT, STAGE, st>>>(a);
+  else bmm_single_kernel<A_K, B_K, FMT, MODE, SB_COL, false><<<a.total_tiles, NT, STAGE, st>>>(a);
   return check_launch("bmm_single_kernel");
 }
 
