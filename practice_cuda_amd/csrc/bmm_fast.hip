@@ -33,6 +33,7 @@
 #include "abi_util.h"
 #include "bmm_epilogue.h"
 #include "bmm_fast.h"
+#include "bmm_lds.h"
 #include "fp8_common.h"
 
 namespace pcamd {
@@ -436,52 +437,53 @@ __global__ __launch_bounds__(NT, STAGED ? 3 : 2) void bmm_single_kernel(FastArgs
   const int m0 = (first_m + in_group % gm) * BM;
   const int n0 = (in_group / gm) * BN;
 
-  const __amdgpu_buffer_rsrc_t rsa = make_rsrc(a.a + bidx * a.sab, a.a_extent);
-  const __amdgpu_buffer_rsrc_t rsb = make_rsrc(a.b + bidx * a.sbb, a.b_extent);
-  if constexpr (A_K) issue_kmajor<BM>(rsa, smem, m0, a.lda, 0, wave, lane);
-  if constexpr (B_K) issue_kmajor<BN>(rsb, smem + A_BYTES, n0, a.ldb, 0, wave, lane);
-  if constexpr (!A_K) {
-    MNStage<BM> st;
-    st.load(rsa, m0, a.lda, 0, t);
-    st.store(smem, t);
-  }
-  if constexpr (!B_K) {
-    MNStage<BN> st;
-    st.load(rsb, n0, a.ldb, 0, t);
-    st.store(smem + A_BYTES, t);
-  }
-
   const int row_base = m0 + wm * 64 + lr;
   const int col_base = n0 + wn * 128 + 4 * lg;
-  // per-row and per-column scales (issued before the wait so they overlap it)
+  // per-row and per-column scales, issued first: the MN-major operand's LDS
+  // store below waits for its loads, and would otherwise expose their latency.
+  // Indices are clamped to the last row / column instead of branching; values
+  // of rows and columns past the matrix are never stored.
   float sav[4], sbv[8][SB_COL || MODE == 1 ? 4 : 1];
+  const float* sa_b = a.sa + bidx * a.ssab;
+  const float* sb_b = a.sb + bidx * a.ssbb;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const int mm = row_base + 16 * i;
-    if constexpr (MODE == 0) sav[i] = mm < a.m ? a.sa[bidx * a.ssab + int64_t(mm >> a.qbm_shift) * a.ssa1] : 0.0f;
-    else if constexpr (MODE == 1) sav[i] = mm < a.m ? a.sa[bidx * a.ssab + int64_t(mm) * a.ssa1] : 0.0f;
+    const int mm = min(row_base + 16 * i, a.m - 1);
+    if constexpr (MODE == 0) sav[i] = sa_b[int64_t(mm >> a.qbm_shift) * a.ssa1];
+    else if constexpr (MODE == 1) sav[i] = sa_b[int64_t(mm) * a.ssa1];
     else sav[i] = 1.0f;
   }
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
     if constexpr (MODE == 0 && !SB_COL) {
-      const int nn = col_base + 16 * j;
-      sbv[j][0] = nn < a.n ? a.sb[bidx * a.ssbb + int64_t(nn >> a.qbn_shift) * a.ssb2] : 0.0f;
+      const int nn = min(col_base + 16 * j, a.n - 1);
+      sbv[j][0] = sb_b[int64_t(nn >> a.qbn_shift) * a.ssb2];
     } else if constexpr (MODE == 0 || MODE == 1) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int nn = col_base + 16 * j + r;
-        if (nn < a.n) {
-          sbv[j][r] = MODE == 0 ? a.sb[bidx * a.ssbb + int64_t(nn >> a.qbn_shift) * a.ssb2]
-                                : a.sb[bidx * a.ssbb + int64_t(nn) * a.ssb1];
-        } else {
-          sbv[j][r] = 0.0f;
-        }
+        const int nn = min(col_base + 16 * j + r, a.n - 1);
+        sbv[j][r] = MODE == 0 ? sb_b[int64_t(nn >> a.qbn_shift) * a.ssb2] : sb_b[int64_t(nn) * a.ssb1];
       }
     } else {
       sbv[j][0] = 1.0f;
     }
   }
+
+  const __amdgpu_buffer_rsrc_t rsa = make_rsrc(a.a + bidx * a.sab, a.a_extent);
+  // An M-major A goes through registers (loads, then byte transposes into the
+  // K-contiguous LDS layout); its loads are issued ahead of the direct-to-LDS
+  // ones so the transposes overlap them. B goes straight to LDS either way:
+  // K-major rows, or N-major k-rows read back with transposing LDS loads.
+  MNStage<BM> sta;
+  if constexpr (!A_K) sta.load(rsa, m0, a.lda, 0, t);
+  if constexpr (A_K) issue_kmajor<BM>(rsa, smem, m0, a.lda, 0, wave, lane);
+  if constexpr (B_K) {
+    issue_kmajor<BN>(make_rsrc(a.b + bidx * a.sbb, a.b_extent), smem + A_BYTES, n0, a.ldb, 0, wave, lane);
+  } else {
+    const lds::MNMajorLoader<BN, NT / 64> lb(a.ldb, lane, wave);
+    lb.issue(lds::make_rsrc(a.b + bidx * a.sbb, a.b_extent), smem + A_BYTES, n0, a.ldb, 0, wave);
+  }
+  if constexpr (!A_K) sta.store(smem, t);
 
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
@@ -504,7 +506,9 @@ __global__ __launch_bounds__(NT, STAGED ? 3 : 2) void bmm_single_kernel(FastArgs
     v4f acc[4][4];
 #pragma unroll
     for (int jj = 0; jj < 4; ++jj) {
-      const v8i bf = frag(smem + A_BYTES, wn * 128 + (4 * h + jj) * 16 + lr, lg);
+      v8i bf;
+      if constexpr (B_K) bf = frag(smem + A_BYTES, wn * 128 + (4 * h + jj) * 16 + lr, lg);
+      else bf = lds::frag_mn<BN>(smem + A_BYTES, wn * 128 + (4 * h + jj) * 16, lane);
 #pragma unroll
       for (int i = 0; i < 4; ++i) acc[i][jj] = mfma<FMT>(bf, af[i], v4f{0.f, 0.f, 0.f, 0.f});
     }

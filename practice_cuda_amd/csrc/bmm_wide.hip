@@ -35,24 +35,27 @@
 #include "abi_util.h"
 #include "bmm_epilogue.h"
 #include "bmm_fast.h"
+#include "bmm_lds.h"
 #include "fp8_common.h"
 
 namespace pcamd {
 namespace bmmw {
 
-typedef int v8i __attribute__((ext_vector_type(8)));
-typedef int v4i __attribute__((ext_vector_type(4)));
-typedef int v2i __attribute__((ext_vector_type(2)));
+using lds::v8i;
+using lds::v4i;
+using lds::make_rsrc;
+using lds::lds_addr;
+using lds::lds_dma16;
+using lds::frag_mn;
 typedef float v4f __attribute__((ext_vector_type(4)));
-typedef __attribute__((address_space(3))) void* lds_ptr_t;
-typedef __attribute__((address_space(3))) v2i* lds_v2i_ptr;
 
 constexpr int NT = 512;
 constexpr int WAVES = NT / 64;
 constexpr int BM = 256, BN = 256, BK = 128;
 constexpr int A_BYTES = BM * BK, B_BYTES = BN * BK;  // 32 KiB each
 constexpr int STAGE = A_BYTES + B_BYTES;
-constexpr uint32_t kRsrcWord3 = 0x00020000u;
+template <int COLS>
+using MNMajorLoader = lds::MNMajorLoader<COLS, WAVES>;
 
 // LDS swizzles. gfx950's LDS serves 256 bytes (64 banks) per cycle.
 // K-major tile (128-byte rows): chunk c of row r sits at position c ^ swz_k(r).
@@ -66,40 +69,6 @@ template <int N>
 using IC = std::integral_constant<int, N>;
 
 PCAMD_DEV int swz_k(int r) { return (((r >> 1) & 1) * 5) ^ ((r >> 2) & 1); }
-// MN-major tile (256-byte k-rows): chunk c of k-row k sits at position
-// c ^ (k & 7) ^ (8 ((k >> 5) & 1)). A 16-lane group reads 8 k-rows k0..k0+7
-// (k0 % 8 == 0) at one 8-byte half pair: k & 7 spreads them over 32 banks,
-// and the group served in the same cycle (k-rows 32 further on) lands in the
-// other 32.
-PCAMD_DEV int swz_mn(int k) { return (k & 7) ^ (((k >> 5) & 1) << 3); }
-
-// Buffer descriptor in four SGPRs: base, byte size (the hardware returns 0
-// for offsets at or past it), raw addressing.
-PCAMD_DEV v4i make_rsrc(const void* base, uint32_t bytes) {
-  const uint64_t p = reinterpret_cast<uint64_t>(base);
-  v4i r;
-  r[0] = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(p));
-  r[1] = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(p >> 32));
-  r[2] = __builtin_amdgcn_readfirstlane(bytes);
-  r[3] = kRsrcWord3;
-  return r;
-}
-
-PCAMD_DEV uint32_t lds_addr(const void* p) {
-  return __builtin_amdgcn_readfirstlane(
-      static_cast<uint32_t>(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const uint8_t*)p)));
-}
-
-// 16 bytes per lane global -> LDS: lane i's bytes land at lds + 16 i. Issued
-// from inline asm on purpose: the compiler's wait-count pass cannot tell
-// that LDS reads of the other stage do not alias these writes and would put
-// a vmcnt(0) in front of every ds_read, serialising prefetch and MFMAs. The
-// kernels order these loads themselves (s_waitcnt vmcnt(0) + barrier before
-// a stage is read, barrier before it is refilled).
-PCAMD_DEV void lds_dma16(v4i rs, uint32_t lds, uint32_t voff) {
-  asm volatile("buffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(voff), "s"(rs), "{m0}"(lds) : "memory");
-}
-
 // Direct-to-LDS loads of one operand tile. The per-lane part of the byte
 // offset is the same for every K step (and, for a K-major tile, for every
 // instruction), so it is computed once; the uniform part - tile origin, K
@@ -131,38 +100,6 @@ struct KMajorLoader {
   }
 };
 
-// MN-major tile: 128 k-rows (k0 + k, stride ld) x COLS bytes from col0.
-// Instruction i of wave w fills k-rows kb = w * 16 + i * R .. + R - 1 (R = 64 /
-// (COLS / 16) rows per instruction); lane l takes k-row kb + l / CHUNKS and LDS
-// slot l % CHUNKS, which holds global chunk slot ^ swz_mn(k). Bit 5 of k is
-// the wave's (w * 16 + i * R + l / CHUNKS < w * 16 + 16), and k & 7 repeats
-// every two instructions, so two lane offsets per wave serve them all.
-template <int COLS>
-struct MNMajorLoader {
-  static constexpr int CHUNKS = COLS / 16;
-  static constexpr int R = 64 / CHUNKS;
-  static constexpr int PER_WAVE = BK / WAVES;
-  static constexpr int INSTS = PER_WAVE / R;
-  static_assert(COLS == 256 && PER_WAVE == 16, "swizzle assumes 256-byte k-rows, 16 per wave");
-  uint32_t voff[2];
-  PCAMD_DEV MNMajorLoader(uint32_t ld, int lane, int wave) {
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const int k = wave * PER_WAVE + h * R + lane / CHUNKS;
-      voff[h] = (lane / CHUNKS) * ld + (((lane % CHUNKS) ^ swz_mn(k)) << 4);
-    }
-  }
-  PCAMD_DEV void issue(v4i rs, uint8_t* tile, uint32_t col0, uint32_t ld, uint32_t k0, int wave) const {
-#pragma unroll
-    for (int i = 0; i < INSTS; ++i) {
-      const int kb = wave * PER_WAVE + i * R;
-      uint32_t u = __builtin_amdgcn_readfirstlane((k0 + kb) * ld + col0);
-      asm volatile("" : "+s"(u));
-      lds_dma16(rs, lds_addr(tile + kb * COLS), voff[i & 1] + u);
-    }
-  }
-};
-
 // fragment of a K-major tile: row `row`, k bytes [32 g, 32 g + 32)
 PCAMD_DEV v8i frag_k(const uint8_t* tile, int row, int g) {
   const uint4* l = reinterpret_cast<const uint4*>(tile + row * BK);
@@ -172,25 +109,6 @@ PCAMD_DEV v8i frag_k(const uint8_t* tile, int row, int g) {
   v8i f;
   f[0] = x.x; f[1] = x.y; f[2] = x.z; f[3] = x.w;
   f[4] = y.x; f[5] = y.y; f[6] = y.z; f[7] = y.w;
-  return f;
-}
-
-// fragment of an MN-major tile (COLS bytes per k-row): column block
-// [col16, col16 + 16) (16-aligned), lane j = lane & 15, k-group g
-template <int COLS>
-PCAMD_DEV v8i frag_mn(const uint8_t* tile, int col16, int lane) {
-  const int g = lane >> 4, j = lane & 15;
-  const int c = col16 >> 4;       // chunk holding the 16 columns
-  const int half = (j & 1) << 3;  // lane pairs cover 8 + 8 columns
-  v8i f;
-#pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    const int k = 32 * g + 8 * q + (j >> 1);
-    const uint8_t* p = tile + k * COLS + ((c ^ swz_mn(k)) << 4) + half;
-    const v2i v = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i_ptr)(p));
-    f[2 * q] = v[0];
-    f[2 * q + 1] = v[1];
-  }
   return f;
 }
 
