@@ -28,6 +28,9 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0        # MI355X HBM3E
+# the kernel pcamd_quant_channel launches for the headline workload (rows of
+# 7168 bf16 elements: one 256-thread workgroup per row, 4 chunk slots per thread)
+HEADLINE_KERNEL = "quant_rowblock_kernel<bf16,e4m3,4,nt>"
 FP8_PEAK_TFLOPS = 5000.0     # MI355X dense fp8 MFMA (5.0 PFLOP/s)
 
 
@@ -355,14 +358,16 @@ def main():
                    "shape": [18432, 7168], "rotating_buffer_sets": 4, "timing": "HIP graph of K launches"},
         "roofline": {"bound": "hbm", "achieved": round(head["value"], 2), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(head["value"] / HBM_PEAK_GBS, 4),
-                     "traffic": None, "kernel": "quant_waverow_kernel<bf16,e4m3,16,nt>",
+                     "traffic": None, "kernel": HEADLINE_KERNEL,
                      "bytes_per_launch": head["bytes_per_step"]},
     }
+    # HBM bytes per launch from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE
+    # passes, used only if they were taken on the kernel that runs now
     traffic_file = os.path.join(ROOT, "profiles", "traffic.json")
     if os.path.exists(traffic_file):
         with open(traffic_file) as fh:
             t = json.load(fh).get("config2_per_channel_quant")
-        if t:
+        if t and t.get("kernel") == HEADLINE_KERNEL:
             line["roofline"]["traffic"] = t["hbm_bytes_per_launch"]
 
     if not args.no_components:
