@@ -120,6 +120,30 @@ def test_bmm_b_block_widths(dev, qbn, b_layout):
     assert O.max_abs_rel(out.float().cpu().numpy(), ref) <= TOL
 
 
+@pytest.mark.parametrize("scheme,layout,qbn", [
+    ("hip_per_block_1d", "a_k_b_k", None),   # per-column B scales
+    ("hip_per_block_2d", "a_k_b_n", None),   # one B scale per 128 columns
+    ("hip_per_block_1d", "a_m_b_n", None),   # both operands MN-major
+    ("direct", "a_k_b_n", 16),               # one B scale per 16 columns
+    ("hip_per_tensor", "a_k_b_k", None),     # one tile per workgroup
+])
+def test_bmm_more_tiles_than_cus(dev, scheme, layout, qbn):
+    # 3 x 5 x 18 = 270 output tiles of 256 x 256, more than MI355X's 256 CUs
+    # (a second wave of workgroups, tiles of three batches), and K = 384: an
+    # odd number of 128-deep K steps
+    print(f"bmm more tiles than CUs {scheme} {layout} qbn={qbn}", flush=True)
+    a, b = rand((3, 1280, 384), 12), rand((3, 384, 4608), 13)
+    if scheme == "direct":
+        qa = hip_per_block_quant(a.to(dev), block_m=1, block_n=128)
+        qb = hip_per_block_quant(b.to(dev), block_m=128, block_n=qbn)
+        out = hip_per_block_bmm(qa, qb)
+        torch.cuda.synchronize()
+        ref = O.bmm_reference(qa.dequantize().double().cpu().numpy(), qb.dequantize().double().cpu().numpy())
+    else:
+        out, ref = run_registered(f"{scheme}_{layout}", a, b, dev)
+    assert O.max_abs_rel(out.float().cpu().numpy(), ref) <= TOL
+
+
 def test_bmm_golden(dev):
     import os
     d = np.load(os.path.join(os.path.dirname(__file__), "golden", "bmm_golden.npz"))
