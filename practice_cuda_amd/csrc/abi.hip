@@ -1,6 +1,7 @@
 // abi.hip - version and error reporting of the C ABI (include/pcamd_fp8.h).
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <cstdarg>
 #include <cstdio>
 
@@ -25,6 +26,22 @@ int check_launch(const char* what) {
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return set_error(PCAMD_ERR_LAUNCH, "%s: %s", what, hipGetErrorString(e));
   return PCAMD_OK;
+}
+
+int device_cu_count() {
+  constexpr int kMaxDevices = 64;
+  static std::atomic<int> cache[kMaxDevices];  // 0: not queried yet
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 0;
+  const bool cached = dev >= 0 && dev < kMaxDevices;
+  if (cached) {
+    const int c = cache[dev].load(std::memory_order_relaxed);
+    if (c > 0) return c;
+  }
+  int n = 0;
+  if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+  if (cached && n > 0) cache[dev].store(n, std::memory_order_relaxed);
+  return n;
 }
 
 }  // namespace pcamd

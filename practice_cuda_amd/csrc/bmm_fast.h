@@ -25,6 +25,7 @@ struct FastArgs {
   int64_t ssab, ssa1, ssa2, ssbb, ssb1, ssb2;
   int32_t qbk, qbm_shift, qbn_shift;
   int32_t tiles_m, tiles_n, tiles_per_batch, total_tiles;
+  int32_t tile_base;           // first tile of a launch that covers a range of tiles
   int32_t c_dtype, bias_dtype, act, scales_are_quant;
 };
 

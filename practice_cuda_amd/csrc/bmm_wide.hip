@@ -7,6 +7,13 @@
 // owns 64 x 128 = 4 x 8 tiles of v_mfma_f32_16x16x128_f8f6f4, issued with the
 // operands swapped so a lane holds four consecutive N outputs of one row.
 //
+// Half tiles: when the last wave of tiles would fill at most half the CUs
+// (e.g. 896 tiles on 256 CUs), those tiles run as a second launch of
+// 256 x 128 halves, two workgroups per tile, each wave computing 64 x 64
+// (JN = 4 sub-tiles instead of 8). A half loads the whole tile's operands -
+// the loaders and LDS layout are the same - and reads the B fragments of its
+// own 128 columns. The last wave then takes about half a tile's time.
+//
 // Both operands go global -> LDS with buffer_load_dwordx4 ... lds (no VGPR
 // staging), one K step ahead of the MFMAs. The LDS layout follows the global
 // one:
@@ -196,8 +203,9 @@ __device__ __attribute__((noinline)) void epilogue_general(void* c, int64_t c_ro
 //     step's first B fragment; the next step's A fragment i is read right
 //     after MFMA (i, 7) has consumed the current one. The last sub-tile's
 //     MFMAs cover the latency of those reads.
-template <bool A_K, bool B_K, int FMT, int MODE, int SBK>
+template <bool A_K, bool B_K, int FMT, int MODE, int SBK, int JN>
 __global__ __launch_bounds__(NT, 1) void bmm_wide_kernel(FastArgs a) {
+  static_assert(JN == 8 || JN == 4, "sub-tiles per wave: 8 (whole tiles) or 4 (half tiles)");
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   float* sa_tile = reinterpret_cast<float*>(smem + 2 * STAGE);  // [2][BM]
   float* sb_tile = sa_tile + 2 * BM;                             // [2][BN]
@@ -206,8 +214,26 @@ __global__ __launch_bounds__(NT, 1) void bmm_wide_kernel(FastArgs a) {
   const int wm = wave & 3, wn = wave >> 2;  // 4 x 2 waves
   const int lr = lane & 15, lg = lane >> 4;
 
+  // Tile index (tiles ordered as below) and the wave's first column in it.
+  // Whole tiles: consecutive tiles land on one XCD (blockIdx % 8 picks it).
+  // Half tiles (tiles tile_base ..): the two halves of a tile go to
+  // workgroups b and b + 8, on the same XCD, so both read its operands
+  // through one L2.
   int pid = blockIdx.x;
-  if ((a.total_tiles & 7) == 0) pid = (pid & 7) * (a.total_tiles >> 3) + (pid >> 3);
+  int wcol = wn * 128;
+  if constexpr (JN == 8) {
+    if ((a.total_tiles & 7) == 0) pid = (pid & 7) * (a.total_tiles >> 3) + (pid >> 3);
+  } else {
+    int hsel;
+    if ((gridDim.x & 15) == 0) {
+      hsel = (pid >> 3) & 1;
+      pid = a.tile_base + ((pid >> 4) << 3) + (pid & 7);
+    } else {
+      hsel = pid & 1;
+      pid = a.tile_base + (pid >> 1);
+    }
+    wcol = __builtin_amdgcn_readfirstlane(hsel * 128 + wn * 64);
+  }
   // (the divisions run on the VALU; the results are workgroup-uniform and are
   // moved back to SGPRs so everything derived from them stays scalar)
   const int bidx = __builtin_amdgcn_readfirstlane(pid / a.tiles_per_batch);
@@ -238,8 +264,8 @@ __global__ __launch_bounds__(NT, 1) void bmm_wide_kernel(FastArgs a) {
     else return frag_mn<BM>(stage, wm * 64 + i * 16, lane);
   };
   auto bfrag = [&](const uint8_t* stage, int j) -> v8i {
-    if constexpr (B_K) return frag_k(stage + A_BYTES, wn * 128 + j * 16 + lr, lg);
-    else return frag_mn<BN>(stage + A_BYTES, wn * 128 + j * 16, lane);
+    if constexpr (B_K) return frag_k(stage + A_BYTES, wcol + j * 16 + lr, lg);
+    else return frag_mn<BN>(stage + A_BYTES, wcol + j * 16, lane);
   };
   // Block scales of K step ks for this thread's slot: waves 0-3 fetch the
   // tile's 256 row scales, waves 4-7 its 256 column scales (the wave index is
@@ -256,11 +282,11 @@ __global__ __launch_bounds__(NT, 1) void bmm_wide_kernel(FastArgs a) {
   auto load_scale = [&](int ks) -> float { return s_ptr[int64_t(ks) * s_kstride]; };  // qbk == 128
   auto store_scale = [&](int ks, float v) { s_tile[(ks & 1) * 256] = v; };
 
-  v4f acc[4][8];
+  v4f acc[4][JN];
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
-    for (int j = 0; j < 8; ++j) acc[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < JN; ++j) acc[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
 
   const int ksteps = a.k / BK;  // >= 2
   // prologue: step 0 resident in stage 0, step 1 in flight to stage 1
@@ -292,7 +318,7 @@ __global__ __launch_bounds__(NT, 1) void bmm_wide_kernel(FastArgs a) {
   }
   cs[0] = cs[1] = float4{0.f, 0.f, 0.f, 0.f};
   const int sa_off = wm * 64 + lr;
-  const int sb_off = wn * 128 + (SBK == 2 ? 4 * lg : 0);
+  const int sb_off = wcol + (SBK == 2 ? 4 * lg : 0);
   auto read_rows = [&](int ks, float (&sa)[4], float (&f)[4]) {
     const float* sat = sa_tile + (ks & 1) * BM + sa_off;
 #pragma unroll
@@ -323,7 +349,7 @@ __global__ __launch_bounds__(NT, 1) void bmm_wide_kernel(FastArgs a) {
   auto subtile = [&](int j, const v8i& bcur, const uint8_t* af_next, auto ds_reads_c, auto next_c) {
     constexpr int ds_reads = decltype(ds_reads_c)::value;
     constexpr bool NEXT = decltype(next_c)::value;
-    const int jp = (j + 7) & 7;
+    const int jp = (j + JN - 1) % JN;
     float cf[4], cc[4];
     if constexpr (MODE == 0) {
       const float4 c = cs[j & 1];
@@ -384,7 +410,7 @@ __global__ __launch_bounds__(NT, 1) void bmm_wide_kernel(FastArgs a) {
     const uint8_t* cur = smem + (ks & 1) * STAGE;
     const uint8_t* nxt = smem + ((ks + 1) & 1) * STAGE;
 #pragma unroll
-    for (int j = 0; j < 7; ++j) {
+    for (int j = 0; j < JN - 1; ++j) {
       const v8i bcur = bf[j & 1];
       bf[(j + 1) & 1] = bfrag(cur, j + 1);
       if constexpr (MODE == 0 && SBK != 0) read_cols(ks, j + 1);
@@ -404,17 +430,17 @@ __global__ __launch_bounds__(NT, 1) void bmm_wide_kernel(FastArgs a) {
         if constexpr (SBK != 0) read_cols(ks + 1, 0);
         float sa_n[4], fc_n[4];
         read_rows(ks + 1, sa_n, fc_n);
-        subtile(7, bf[1], nxt, IC<kBReads + (SBK != 0 ? 1 : 0) + (SBK == 0 ? 3 : 2)>{}, T{});
+        subtile(JN - 1, bf[1], nxt, IC<kBReads + (SBK != 0 ? 1 : 0) + (SBK == 0 ? 3 : 2)>{}, T{});
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           sa_c[i] = sa_n[i];
           fc[i] = fc_n[i];
         }
       } else {
-        subtile(7, bf[1], nxt, IC<kBReads>{}, T{});
+        subtile(JN - 1, bf[1], nxt, IC<kBReads>{}, T{});
       }
     } else {
-      subtile(7, bf[1], nullptr, IC<0>{}, F{});
+      subtile(JN - 1, bf[1], nullptr, IC<0>{}, F{});
     }
   };
   for (int ks = 0; ks < ksteps - 2; ++ks) step(ks, T{}, T{});
@@ -424,11 +450,11 @@ __global__ __launch_bounds__(NT, 1) void bmm_wide_kernel(FastArgs a) {
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) acc[i][7][r] += p[i][r] * (SBK == 2 ? pf[i] * pc[r] : pf[i]);
+      for (int r = 0; r < 4; ++r) acc[i][JN - 1][r] += p[i][r] * (SBK == 2 ? pf[i] * pc[r] : pf[i]);
   }
 
   const int row_base = m0 + wm * 64 + lr;
-  const int col_base = n0 + wn * 128 + 4 * lg;
+  const int col_base = n0 + wcol + 4 * lg;
 
   // ---- epilogue ----
   float tscale = 1.0f;
@@ -466,17 +492,23 @@ __global__ __launch_bounds__(NT, 1) void bmm_wide_kernel(FastArgs a) {
   };
   const bool plain = a.bias == nullptr && a.act == PCAMD_ACT_NONE && a.c_dtype == kBF16;
   if (staged_output_ok(a.c, a.scb, a.scm, a.n, plain)) {
-    // each wave stages its sub-tile in 8 KiB of the LDS stage the last K step
-    // did not read (no other wave touches it, so no barrier is needed)
+    // each wave stages its sub-tile in 8 KiB (4 KiB for a half tile) of the
+    // LDS stage the last K step did not read (no other wave touches it, so no
+    // barrier is needed)
     const float sam_v[4] = {row_scale(0), row_scale(1), row_scale(2), row_scale(3)};
-    store_subtile_staged(smem + (ksteps & 1) * STAGE + wave * 8192,
-                         reinterpret_cast<__bf16*>(a.c) + bidx * a.scb, a.scm, a.m, a.n, m0 + wm * 64,
-                         n0 + wn * 128, lane, [&](int i, int j, float (&v)[4]) {
-                           float sbv[4];
-                           col_scales(j, sbv);
+    auto value = [&](int i, int j, float (&v)[4]) {
+      float sbv[4];
+      col_scales(j, sbv);
 #pragma unroll
-                           for (int r = 0; r < 4; ++r) v[r] = out_value(i, j, r, sam_v[i], sbv);
-                         });
+      for (int r = 0; r < 4; ++r) v[r] = out_value(i, j, r, sam_v[i], sbv);
+    };
+    __bf16* cb = reinterpret_cast<__bf16*>(a.c) + bidx * a.scb;
+    if constexpr (JN == 8)
+      store_subtile_staged(smem + (ksteps & 1) * STAGE + wave * 8192, cb, a.scm, a.m, a.n, m0 + wm * 64,
+                           n0 + wcol, lane, value);
+    else
+      store_half_staged(smem + (ksteps & 1) * STAGE + wave * 4096, cb, a.scm, a.m, a.n, m0 + wm * 64, n0 + wcol,
+                        lane, value);
     return;
   }
 #pragma unroll
@@ -484,7 +516,7 @@ __global__ __launch_bounds__(NT, 1) void bmm_wide_kernel(FastArgs a) {
     const int mm = row_base + 16 * i;
     const float sam_v = row_scale(i);
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
+    for (int j = 0; j < JN; ++j) {
       const int nn = col_base + 16 * j;
       float sbv[4];
       col_scales(j, sbv);
@@ -506,9 +538,9 @@ __global__ __launch_bounds__(NT, 1) void bmm_wide_kernel(FastArgs a) {
 
 constexpr int LDS_BYTES = 2 * STAGE + 2 * (BM + BN) * 4;
 
-template <bool A_K, bool B_K, int FMT, int MODE, int SBK>
-int launch_one(const FastArgs& a, hipStream_t st) {
-  auto kern = bmm_wide_kernel<A_K, B_K, FMT, MODE, SBK>;
+template <bool A_K, bool B_K, int FMT, int MODE, int SBK, int JN>
+int launch_tiles(const FastArgs& a, int grid, hipStream_t st) {
+  auto kern = bmm_wide_kernel<A_K, B_K, FMT, MODE, SBK, JN>;
   static bool configured = false;  // benign race: the attribute call is idempotent
   if (!configured) {
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
@@ -516,8 +548,25 @@ int launch_one(const FastArgs& a, hipStream_t st) {
     if (e != hipSuccess) return set_error(PCAMD_ERR_LAUNCH, "hipFuncSetAttribute: %s", hipGetErrorString(e));
     configured = true;
   }
-  kern<<<a.total_tiles, NT, LDS_BYTES, st>>>(a);
+  kern<<<grid, NT, LDS_BYTES, st>>>(a);
   return check_launch("bmm_wide_kernel");
+}
+
+// One workgroup per tile (one per CU at a time: the LDS stages allow no
+// more). When the last wave of tiles would occupy at most half the CUs, it
+// runs as a second launch of half tiles instead.
+template <bool A_K, bool B_K, int FMT, int MODE, int SBK>
+int launch_one(const FastArgs& a, hipStream_t st) {
+  const int cus = device_cu_count();
+  const int tail = cus > 0 && a.total_tiles > cus ? a.total_tiles % cus : 0;
+  if (tail == 0 || 2 * tail > cus) return launch_tiles<A_K, B_K, FMT, MODE, SBK, 8>(a, a.total_tiles, st);
+  FastArgs whole = a;
+  whole.total_tiles = a.total_tiles - tail;  // the XCD remap spans the whole tiles only
+  int rc = launch_tiles<A_K, B_K, FMT, MODE, SBK, 8>(whole, whole.total_tiles, st);
+  if (rc != 0) return rc;
+  FastArgs half = a;
+  half.tile_base = a.total_tiles - tail;
+  return launch_tiles<A_K, B_K, FMT, MODE, SBK, 4>(half, 2 * tail, st);
 }
 
 // block mode: B-scale kind from the quant block width (qbn = 1 << qbn_shift):

@@ -120,19 +120,22 @@ def test_bmm_b_block_widths(dev, qbn, b_layout):
     assert O.max_abs_rel(out.float().cpu().numpy(), ref) <= TOL
 
 
+@pytest.mark.parametrize("shape", [(3, 1280, 384, 4608), (1, 2816, 256, 6144)])
 @pytest.mark.parametrize("scheme,layout,qbn", [
     ("hip_per_block_1d", "a_k_b_k", None),   # per-column B scales
     ("hip_per_block_2d", "a_k_b_n", None),   # one B scale per 128 columns
     ("hip_per_block_1d", "a_m_b_n", None),   # both operands MN-major
     ("direct", "a_k_b_n", 16),               # one B scale per 16 columns
-    ("hip_per_tensor", "a_k_b_k", None),     # one tile per workgroup
+    ("hip_per_tensor", "a_k_b_k", None),
 ])
-def test_bmm_more_tiles_than_cus(dev, scheme, layout, qbn):
-    # 3 x 5 x 18 = 270 output tiles of 256 x 256, more than MI355X's 256 CUs
-    # (a second wave of workgroups, tiles of three batches), and K = 384: an
-    # odd number of 128-deep K steps
-    print(f"bmm more tiles than CUs {scheme} {layout} qbn={qbn}", flush=True)
-    a, b = rand((3, 1280, 384), 12), rand((3, 384, 4608), 13)
+def test_bmm_more_tiles_than_cus(dev, shape, scheme, layout, qbn):
+    # 3 x 5 x 18 = 270 and 11 x 24 = 264 output tiles of 256 x 256: more than
+    # MI355X's 256 CUs, so the last 14 / 8 tiles run as half tiles (28 / 16
+    # workgroups: both ways of pairing halves). The first shape also has three
+    # batches and an odd number (3) of 128-deep K steps.
+    b_, m, k, n = shape
+    print(f"bmm more tiles than CUs {shape} {scheme} {layout} qbn={qbn}", flush=True)
+    a, b = rand((b_, m, k), 12), rand((b_, k, n), 13)
     if scheme == "direct":
         qa = hip_per_block_quant(a.to(dev), block_m=1, block_n=128)
         qb = hip_per_block_quant(b.to(dev), block_m=128, block_n=qbn)
