@@ -16,9 +16,12 @@
 //   quant_tile_kernel   one workgroup per block_m x block_n block held in
 //                       registers (e.g. 128 x 128 = 8 chunks per thread);
 //                       wave DPP max, then an LDS max across the 4 waves.
-//   quant_cols_kernel   row-contiguous input with column groups (block_n = 1,
-//                       16 <= block_m <= 256, held in registers) or whole
-//                       columns (channel_axis = -1, two passes over the strip).
+//   quant_colgroup_kernel  row-contiguous input with column groups
+//                       (block_n = 1, 16 <= block_m <= 256): one 128-column
+//                       strip of one row group per workgroup, held in registers.
+//   quant_cols_kernel   whole columns (channel_axis = -1, two passes over the
+//                       strip), and column groups on grids too large for the
+//                       column-group kernel's 3-D grid.
 //   quant_*_generic     any strides / block shape; one workgroup per block or
 //                       channel, two passes (second read served by L2).
 //   per-tensor          amax kernel (workgroup max + one atomic max on the
@@ -560,6 +563,82 @@ __global__ void selftest_init_kernel(uint32_t* result) {
 }
 
 // ===========================================================================
+// column-group kernel: block_m x 1 groups (block_m = 16 .. 256), one
+// 128-column strip of one row group per workgroup
+// ===========================================================================
+// Grid (strips, row groups, batch). Lane l of a 16-lane row slice takes
+// columns 8 l .. 8 l + 7 of the strip, slice s (16 per workgroup) rows
+// s, s + 16, ... of the group: CPT = block_m / 16 chunks per lane, loaded up
+// front and held in registers. Column maxima: the four slices of a wave meet
+// through lane shuffles (xor 16, 32), the four waves through LDS; 128 lanes
+// then form one column's scales each. FULL: m and n are multiples of the
+// group and the strip, so no bounds checks.
+template <int DT, int FMT, int CPT, bool NTS, bool FULL>
+__global__ __launch_bounds__(kThreads) void quant_colgroup_kernel(ColArgs a) {
+  constexpr int EB = elem_bytes<DT>();
+  constexpr int WAVES = kThreads / 64;
+  __shared__ float part[WAVES][128];
+  __shared__ float qsv[128];
+  const int t = threadIdx.x;
+  const int lc = t & 15, rs = t >> 4;
+  const int64_t b = blockIdx.z, g = blockIdx.y, strip = blockIdx.x;
+  const int64_t col = strip * 128 + lc * 8;
+  const int64_t r0 = g * (CPT * 16);
+  const char* xb = a.x + b * a.sxb * EB;
+  Chunk<DT> raw[CPT];
+#pragma unroll
+  for (int p = 0; p < CPT; ++p) {
+    const int64_t r = r0 + p * 16 + rs;
+    if (FULL || (r < a.m && col < a.n)) load_chunk<DT>(raw[p], xb + (r * a.sxm + col) * EB);
+    else zero_chunk<DT>(raw[p]);
+  }
+  float cmax[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+  for (int p = 0; p < CPT; ++p) {
+    float v[8];
+    unpack_chunk<DT>(raw[p], v);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) cmax[i] = fmaxf(cmax[i], fabsf(v[i]));
+  }
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    cmax[i] = fmaxf(cmax[i], __shfl_xor(cmax[i], 16));
+    cmax[i] = fmaxf(cmax[i], __shfl_xor(cmax[i], 32));
+  }
+  if ((t & 63) < 16) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) part[t >> 6][lc * 8 + i] = cmax[i];
+  }
+  __syncthreads();
+  if (t < 128) {
+    float mx = part[0][t];
+#pragma unroll
+    for (int w = 1; w < WAVES; ++w) mx = fmaxf(mx, part[w][t]);
+    const Scales sc = block_scales(mx, a.fp8_max, a.eps);
+    qsv[t] = sc.qs;
+    const int64_t c = strip * 128 + t;
+    if (FULL || c < a.n) a.scale[b * a.ssb + g * a.ssm + c * a.ssn] = sc.ds;
+  }
+  __syncthreads();
+  float qs[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) qs[i] = qsv[lc * 8 + i];
+  uint8_t* yb = a.y + b * a.syb;
+#pragma unroll
+  for (int p = 0; p < CPT; ++p) {
+    const int64_t r = r0 + p * 16 + rs;
+    if (FULL || (r < a.m && col < a.n)) {
+      float v[8];
+      unpack_chunk<DT>(raw[p], v);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) v[i] = clamp_sym(v[i] * qs[i], a.fp8_max);
+      store8<DT, NTS>(yb + r * a.sym + col,
+                      make_uint2(pack4<FMT>(v[0], v[1], v[2], v[3]), pack4<FMT>(v[4], v[5], v[6], v[7])));
+    }
+  }
+}
+
+// ===========================================================================
 // host dispatch helpers
 // ===========================================================================
 inline int grid_for(int64_t units, int64_t per_block = 1, int64_t cap = 1 << 20) {
@@ -678,6 +757,31 @@ struct LaunchTile {
     }
   }
   static int run(const TileArgs& a, hipStream_t st) { return nt_stores() ? by_cpt<true>(a, st) : by_cpt<false>(a, st); }
+};
+
+template <int DT, int FMT>
+struct LaunchColGroups {
+  template <int CPT, bool NTS>
+  static int go(const ColArgs& a, hipStream_t st) {
+    const dim3 grid(static_cast<uint32_t>(a.strips), static_cast<uint32_t>(a.groups),
+                    static_cast<uint32_t>(a.units / (a.groups * a.strips)));
+    const bool full = a.m % (CPT * 16) == 0 && a.n % 128 == 0;
+    if (full) quant_colgroup_kernel<DT, FMT, CPT, NTS, true><<<grid, kThreads, 0, st>>>(a);
+    else quant_colgroup_kernel<DT, FMT, CPT, NTS, false><<<grid, kThreads, 0, st>>>(a);
+    return check_launch("quant_colgroup_kernel");
+  }
+  template <bool NTS>
+  static int by_cpt(const ColArgs& a, hipStream_t st) {
+    switch (a.rpt) {
+      case 1: return go<1, NTS>(a, st);
+      case 2: return go<2, NTS>(a, st);
+      case 4: return go<4, NTS>(a, st);
+      case 8: return go<8, NTS>(a, st);
+      case 16: return go<16, NTS>(a, st);
+      default: return set_error(PCAMD_ERR_UNSUPPORTED, "column groups: unsupported rows per lane %d", a.rpt);
+    }
+  }
+  static int run(const ColArgs& a, hipStream_t st) { return nt_stores() ? by_cpt<true>(a, st) : by_cpt<false>(a, st); }
 };
 
 template <int DT, int FMT>
@@ -816,6 +920,8 @@ extern "C" int pcamd_quant_block(const void* x, int x_dtype, int64_t batch, int6
     a.group_rows = static_cast<int32_t>(block_m);
     a.rpt = static_cast<int32_t>(block_m / 16);
     a.fp8_max = fp8_max; a.eps = eps;
+    if (a.strips <= INT32_MAX && mb <= 65535 && batch <= 65535)
+      return dispatch_dt_fmt<LaunchColGroups>(x_dtype, y_dtype, a, st);
     return dispatch_dt_fmt<LaunchCols>(x_dtype, y_dtype, a, false, st);
   }
   GenArgs a{};

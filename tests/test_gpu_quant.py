@@ -124,6 +124,7 @@ BLOCK_CASES = [
     ((1000, 136), "bf16", 128, 1, "e4m3"),      # column groups, ragged
     ((2, 512, 264), "f16", 256, 1, "e4m3"),     # column groups, 256x1
     ((96, 64), "bf16", 16, 1, "e4m3"),          # column groups, 16x1
+    ((3, 192, 520), "f32", 64, 1, "e5m2"),      # column groups, 64x1, fp32, ragged strip
     ((200, 300), "bf16", 128, 128, "e4m3"),     # generic (n % 8 != 0)
     ((33, 70), "f32", 4, 32, "e4m3"),           # generic
     ((2, 64, 256), "bf16", 2, 128, "e4m3"),     # generic (2x128)
@@ -155,7 +156,7 @@ def test_block_quant_strided_input(dev):
     assert_same(r, q_ref, s_ref, "transposed")
 
 
-@pytest.mark.parametrize("bm,bn", [(1, 128), (1, 64), (128, 128)])
+@pytest.mark.parametrize("bm,bn", [(1, 128), (1, 64), (128, 128), (128, 1), (32, 1)])
 def test_block_quant_padded_rows(dev, bm, bn):
     # rows contiguous but with a row pitch wider than the row (a column slice of
     # a wider 3-D tensor): the row-indexed kernels, not the flat one
@@ -192,6 +193,20 @@ def test_config1_full_size(dev):
     q_ref, s_ref = O.quant_block(x, 1, 128, threads=8)
     assert r.dequant_scale.shape == (4096, 56)
     assert_same(r, q_ref, s_ref, "config1")
+
+
+def test_column_groups_full_size(dev):
+    """128x1 groups (the wgrad operand quantization) over the config-1 input
+    shape: bf16 [4096, 7168], N(0,1) with 0.1% outliers x50."""
+    g = torch.Generator().manual_seed(1)
+    x = torch.randn(4096, 7168, generator=g)
+    m = torch.rand(4096, 7168, generator=g) < 0.001
+    x[m] *= 50
+    x = x.bfloat16()
+    r = hip_per_block_quant(x.to(dev), block_m=128, block_n=1)
+    q_ref, s_ref = O.quant_block(x, 128, 1, threads=8)
+    assert r.dequant_scale.shape == (32, 7168)
+    assert_same(r, q_ref, s_ref, "128x1 full size")
 
 
 def test_config3_full_size(dev):
