@@ -230,19 +230,8 @@ __global__ __launch_bounds__(kThreads) void quant_tile_kernel(TileArgs a) {
   const int t = threadIdx.x;
   const int lr = t & (a.lpr - 1), rp = t >> a.lpr_shift;  // lane in row, row in pass
   const int rpp = kThreads >> a.lpr_shift;                 // rows per pass
-  int it = 0;
-  for (uint32_t blk = blockIdx.x; blk < a.blocks; blk += gridDim.x, ++it) {
-    uint32_t b, pm, pn;
-    if constexpr (GRID3) {
-      b = blockIdx.z;
-      pm = blockIdx.y;
-      pn = blockIdx.x;
-    } else {
-      b = blk / (a.mb * a.nb);
-      const uint32_t rem = blk - b * a.mb * a.nb;
-      pm = rem / a.nb;
-      pn = rem - pm * a.nb;
-    }
+  // block (pm, pn) of batch b; rd: this block's slot of the cross-wave maxima
+  auto block = [&](uint32_t b, uint32_t pm, uint32_t pn, float* rd) {
     const int64_t r0 = int64_t(pm) * a.block_m;
     const int64_t col = int64_t(pn) * (a.lpr * 8) + lr * 8;
     const char* xb = a.x + int64_t(b) * a.sxb * EB;
@@ -257,7 +246,6 @@ __global__ __launch_bounds__(kThreads) void quant_tile_kernel(TileArgs a) {
 #pragma unroll
     for (int p = 0; p < CPT; ++p) amax = fmaxf(amax, chunk_amax<DT>(cur[p]));
     amax = group_max<64>(amax);
-    float* rd = red[it & 1];  // alternating slots: one barrier per block
     if ((t & 63) == 0) rd[t >> 6] = amax;
     __syncthreads();
     amax = fmaxf(fmaxf(rd[0], rd[1]), fmaxf(rd[2], rd[3]));
@@ -270,7 +258,18 @@ __global__ __launch_bounds__(kThreads) void quant_tile_kernel(TileArgs a) {
       if (FULL || (r < a.m && col < a.n))
         store8<DT, NTS>(yb + r * a.sym + col, quant_chunk<DT, FMT>(cur[p], s.qs, a.fp8_max));
     }
-    if constexpr (GRID3) break;
+  };
+  if constexpr (GRID3) {
+    // no loop: nothing to load before the block's own loads are issued
+    block(blockIdx.z, blockIdx.y, blockIdx.x, red[0]);
+  } else {
+    int it = 0;
+    for (uint32_t blk = blockIdx.x; blk < a.blocks; blk += gridDim.x, ++it) {
+      const uint32_t b = blk / (a.mb * a.nb);
+      const uint32_t rem = blk - b * a.mb * a.nb;
+      const uint32_t pm = rem / a.nb;
+      block(b, pm, rem - pm * a.nb, red[it & 1]);  // alternating slots: one barrier per block
+    }
   }
 }
 
