@@ -11,8 +11,9 @@
 //                       their amax with DPP.
 //   quant_waverow_kernel   per-channel along rows (channel_axis = -2), rows
 //                       of up to 2048 elements: one wave per row.
-//   quant_rowblock_kernel  per-channel along rows, up to 16384 elements: one
-//                       workgroup per row, DPP + one LDS max.
+//   quant_rowblock_kernel  per-channel along rows, 2048 to 16384 elements: one
+//                       workgroup per row sized to two chunks per lane, DPP +
+//                       one LDS max.
 //   quant_tile_kernel   one workgroup per block_m x block_n block held in
 //                       registers (e.g. 128 x 128 = 8 chunks per thread);
 //                       wave DPP max, then an LDS max across the 4 waves.
@@ -169,18 +170,27 @@ __global__ __launch_bounds__(kThreads) void quant_waverow_kernel(RowArgs a) {
 // Per-channel along the row: one workgroup per row, thread t owning chunks
 // t, t + 256, ... (CPT of them, 256 * CPT >= chunks). Wave DPP max, then one
 // LDS exchange across the four waves.
-template <int DT, int FMT, int CPT, bool NTS>
-__global__ __launch_bounds__(kThreads) void quant_rowblock_kernel(RowArgs a) {
+// GRID2: grid (rows, batch), so the row and batch come from the workgroup
+// index with no division ahead of the loads; otherwise a 1-D grid of
+// batch * rows.
+template <int DT, int FMT, int CPT, bool NTS, bool GRID2>
+__global__ __launch_bounds__(1024) void quant_rowblock_kernel(RowArgs a) {
   constexpr int EB = elem_bytes<DT>();
-  __shared__ float red[kThreads / 64];
-  const int t = threadIdx.x;
-  const uint32_t row = blockIdx.x;  // grid = rows
-  const uint32_t b = row / a.m, mi = row - b * a.m;
+  __shared__ float red[1024 / 64];
+  const int t = threadIdx.x, nt = blockDim.x;  // nt: a multiple of 64, CPT * nt >= chunks
+  uint32_t b, mi;
+  if constexpr (GRID2) {
+    b = blockIdx.y;
+    mi = blockIdx.x;
+  } else {
+    b = blockIdx.x / a.m;
+    mi = blockIdx.x - b * a.m;
+  }
   const char* xrow = a.x + (int64_t(b) * a.sxb + int64_t(mi) * a.sxm) * EB;
   Chunk<DT> cur[CPT];
 #pragma unroll
   for (int c = 0; c < CPT; ++c) {
-    const int ch = t + c * kThreads;
+    const int ch = t + c * nt;
     if (ch < a.chunks) load_chunk<DT>(cur[c], xrow + int64_t(ch) * 8 * EB);
     else zero_chunk<DT>(cur[c]);
   }
@@ -190,13 +200,14 @@ __global__ __launch_bounds__(kThreads) void quant_rowblock_kernel(RowArgs a) {
   amax = group_max<64>(amax);
   if ((t & 63) == 0) red[t >> 6] = amax;
   __syncthreads();
-  amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  amax = red[0];
+  for (int w = 1; w < (nt >> 6); ++w) amax = fmaxf(amax, red[w]);
   const Scales s = channel_scales(amax, a.fp8_max, a.eps);
   if (t == 0) a.scale[int64_t(b) * a.ssb + int64_t(mi) * a.ssm] = s.ds;
   uint8_t* yrow = a.y + int64_t(b) * a.syb + int64_t(mi) * a.sym;
 #pragma unroll
   for (int c = 0; c < CPT; ++c) {
-    const int ch = t + c * kThreads;
+    const int ch = t + c * nt;
     if (ch < a.chunks) store8<DT, NTS>(yrow + int64_t(ch) * 8, quant_chunk<DT, FMT>(cur[c], s.qs, a.fp8_max));
   }
 }
@@ -705,8 +716,12 @@ struct LaunchGroups {
 template <int DT, int FMT>
 struct LaunchRowBlock {
   template <int CPT, bool NTS>
-  static int go(const RowArgs& a, hipStream_t st) {
-    quant_rowblock_kernel<DT, FMT, CPT, NTS><<<a.units, kThreads, 0, st>>>(a);
+  static int go(const RowArgs& a, int threads, hipStream_t st) {
+    const uint32_t batch = a.units / a.m;
+    if (batch <= 65535 && a.m <= 0x7FFFFFFFu)
+      quant_rowblock_kernel<DT, FMT, CPT, NTS, true><<<dim3(a.m, batch), threads, 0, st>>>(a);
+    else
+      quant_rowblock_kernel<DT, FMT, CPT, NTS, false><<<a.units, threads, 0, st>>>(a);
     return check_launch("quant_rowblock_kernel");
   }
   template <int MAXC, bool NTS>
@@ -717,14 +732,15 @@ struct LaunchRowBlock {
   }
   template <bool NTS>
   static int pick(const RowArgs& a, hipStream_t st) {
-    // rows up to 2048 elements: one wave per row; longer: a workgroup per row
-    // (measured 2-12% faster than one wave per row at 7168 elements)
-    if (a.cpl <= 4) return wave<4, NTS>(a, st);
-    const int cpt = (a.chunks + kThreads - 1) / kThreads;
-    if (cpt <= 1) return go<1, NTS>(a, st);
-    if (cpt <= 2) return go<2, NTS>(a, st);
-    if (cpt <= 4) return go<4, NTS>(a, st);
-    return go<8, NTS>(a, st);
+    // Rows shorter than 2048 elements: one wave per row. Longer (up to 16384):
+    // one workgroup per row, two chunks per lane, the workgroup size the
+    // smallest multiple of 64 that covers the row. A sweep over 2048-16384
+    // elements: 1-5 % faster than 256-thread workgroups with 2-8 chunks per
+    // lane, and than one wave per row at 2048 (7168: 448 threads, no idle
+    // chunk slot, 68.6 -> 66.6 us on the config-2 tensor).
+    if (a.chunks < 256) return wave<4, NTS>(a, st);
+    const int threads = ((a.chunks + 1) / 2 + 63) / 64 * 64;  // <= 1024: chunks <= 2048
+    return go<2, NTS>(a, threads, st);
   }
   static int run(const RowArgs& a, hipStream_t st) { return nt_stores() ? pick<true>(a, st) : pick<false>(a, st); }
 };
