@@ -127,6 +127,7 @@ def test_bmm_b_block_widths(dev, qbn, b_layout):
     ("hip_per_block_1d", "a_m_b_n", None),   # both operands MN-major
     ("direct", "a_k_b_n", 16),               # one B scale per 16 columns
     ("hip_per_tensor", "a_k_b_k", None),
+    ("hip_per_channel", "a_k_b_k", None),
 ])
 def test_bmm_more_tiles_than_cus(dev, shape, scheme, layout, qbn):
     # 3 x 5 x 18 = 270 and 11 x 24 = 264 output tiles of 256 x 256: more than
@@ -144,6 +145,25 @@ def test_bmm_more_tiles_than_cus(dev, shape, scheme, layout, qbn):
         ref = O.bmm_reference(qa.dequantize().double().cpu().numpy(), qb.dequantize().double().cpu().numpy())
     else:
         out, ref = run_registered(f"{scheme}_{layout}", a, b, dev)
+    assert O.max_abs_rel(out.float().cpu().numpy(), ref) <= TOL
+
+
+@pytest.mark.parametrize("shape", [(2, 200, 128, 300), (2, 260, 640, 520), (3, 1280, 384, 4608)])
+@pytest.mark.parametrize("b_layout", ["n", "k"])
+def test_bmm_e5m2(dev, shape, b_layout):
+    # e5m2 x e5m2 (the reference requires one fp8 dtype for both operands):
+    # the single-step kernel (K = 128), the 256 x 256 kernel, and a grid whose
+    # last tiles run as half tiles
+    b_, m, k, n = shape
+    print(f"bmm e5m2 {shape} b_layout {b_layout}", flush=True)
+    a, b = rand((b_, m, k), 14), rand((b_, k, n), 15)
+    qa = hip_per_block_quant(a.to(dev), block_m=1, block_n=128, fp8_dtype=torch.float8_e5m2)
+    b_in = materialize(b, "k_of_b") if b_layout == "k" else b
+    qb = hip_per_block_quant(b_in.to(dev), block_m=128, block_n=128, fp8_dtype=torch.float8_e5m2)
+    assert qa.tensor.dtype == torch.float8_e5m2 and qb.tensor.dtype == torch.float8_e5m2
+    out = hip_per_block_bmm(qa, qb)
+    torch.cuda.synchronize()
+    ref = O.bmm_reference(qa.dequantize().double().cpu().numpy(), qb.dequantize().double().cpu().numpy())
     assert O.max_abs_rel(out.float().cpu().numpy(), ref) <= TOL
 
 
