@@ -154,6 +154,37 @@ def quant_block_launcher(torch, L, xs, ys, ss, bm, bn):
     return launch
 
 
+def quant_dual_launcher(torch, L, xs, yrs, ycs, srs, scs):
+    def launch(i):
+        x = xs[i % len(xs)]
+        yr, yc, sr, sc = yrs[i % len(yrs)], ycs[i % len(ycs)], srs[i % len(srs)], scs[i % len(scs)]
+        rc = L.lib().pcamd_quant_block_dual(
+            L.ptr(x), L.BF16, 1, x.shape[0], x.shape[1], 0, x.stride(0), 1,
+            L.ptr(yr), L.ptr(yc), L.E4M3FN, 0, yr.stride(0), 1,
+            L.ptr(sr), 0, sr.stride(0), 1, L.ptr(sc), 0, sc.stride(0), 1, 128, 448.0, 1e-12,
+            L.stream_of(x))
+        L.check(rc, "pcamd_quant_block_dual")
+    return launch
+
+
+def bench_quant_dual(torch, name, x_dev, steps, warmup, nsets, dev):
+    """1x128 and 128x1 quantization of one bf16 [m, n] tensor in one kernel."""
+    from practice_cuda_amd import _lib as L
+    m, n = x_dev.shape
+    xs = [x_dev] + [x_dev.view(torch.int16).bitwise_xor(i & 1).view(torch.bfloat16) for i in range(1, nsets)]
+    yrs = [torch.empty(m, n, dtype=torch.float8_e4m3fn, device=dev) for _ in range(nsets)]
+    ycs = [torch.empty(m, n, dtype=torch.float8_e4m3fn, device=dev) for _ in range(nsets)]
+    srs = [torch.empty(m, n // 128, dtype=torch.float32, device=dev) for _ in range(nsets)]
+    scs = [torch.empty(m // 128, n, dtype=torch.float32, device=dev) for _ in range(nsets)]
+    ms, samples = graph_time(torch, quant_dual_launcher(torch, L, xs, yrs, ycs, srs, scs), steps, warmup)
+    nbytes = m * n * 2 + 2 * m * n + 4 * (m * (n // 128) + (m // 128) * n)
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    del xs, yrs, ycs, srs, scs
+    torch.cuda.empty_cache()
+    return {"name": name, "ms_per_step": ms, "bytes_per_step": nbytes, "value": gbs, "unit": "GB/s",
+            "frac_of_hbm_peak": gbs / HBM_PEAK_GBS}
+
+
 def bench_quant(torch, name, x_cpu, kind, steps, warmup, nsets, dev, bm=1, bn=128, settle_ms=0.0):
     from practice_cuda_amd import _lib as L
     m, n = x_cpu.shape
@@ -255,17 +286,27 @@ def bench_config5(torch, steps, warmup, dev):
         res[name] = {"ms": ms, "TFLOP/s": t, "frac_of_fp8_peak": t / FP8_PEAK_TFLOPS}
     total_ms = sum(r["ms"] for r in res.values())
     tflops = 3 * flops / (total_ms * 1e-3) / 1e12
+    del qx, qw, qdy, qdy_m, qx_m, wt, dyt, out_f, out_d, out_w, gemms
+    torch.cuda.empty_cache()
+    # the layer step's quantization launches: X and dY each quantized 1x128
+    # and 128x1 by one kernel, W 128x128
+    quants = [bench_quant_dual(torch, "x_dual_1x128_128x1", X, steps, warmup, 4, dev),
+              bench_quant_dual(torch, "dy_dual_1x128_128x1", dY, steps, warmup, 4, dev),
+              bench_quant(torch, "w_128x128", W.cpu(), "block", steps, warmup, 4, dev, bm=128, bn=128)]
+    for q in quants:
+        q.pop("samples_ms", None)
     layer = layer_step(torch, X, W, dY, steps, dev)
     layer["TFLOP/s"] = 3 * flops / (layer["ms"] * 1e-3) / 1e12
     return {"name": "config5_training_linear_m8192_k4096_n14336", "ms_per_step": total_ms,
             "value": tflops, "unit": "TFLOP/s", "frac_of_fp8_peak": tflops / FP8_PEAK_TFLOPS,
-            "gemms": res, "flops_per_step": 3 * flops, "layer_step": layer}
+            "gemms": res, "flops_per_step": 3 * flops, "quant": quants, "layer_step": layer}
 
 
 def layer_step(torch, X, W, dY, steps, dev):
-    """Forward + backward of Float8BMMLinear at the config-5 shape: the five
-    fp8 quantization passes (X 1x128, W 128x128, dY 1x128, dY and X 128x1)
-    and the three GEMMs, eager (autograd), timed with events."""
+    """Forward + backward of Float8BMMLinear at the config-5 shape: three fp8
+    quantization launches (X 1x128 + 128x1 in one kernel, W 128x128, dY
+    1x128 + 128x1 in one kernel) and the three GEMMs, eager (autograd), timed
+    with events."""
     from practice_cuda_amd.modules import Float8BMMLinear
     layer = Float8BMMLinear(1, X.shape[1], W.shape[0], bias=False, device=dev, dtype=torch.bfloat16)
     with torch.no_grad():
@@ -288,7 +329,8 @@ def layer_step(torch, X, W, dY, steps, dev):
     end.record()
     torch.cuda.synchronize()
     return {"ms": start.elapsed_time(end) / steps,
-            "what": "Float8BMMLinear forward + backward, 5 quantization passes + 3 GEMMs, eager"}
+            "what": "Float8BMMLinear forward + backward, 3 quantization launches (X and dY each 1x128 + 128x1 "
+                    "in one kernel, W 128x128) + 3 GEMMs, eager"}
 
 
 # ---------------------------------------------------------------------------

@@ -33,6 +33,7 @@ EXPORTED_SYMBOLS = (
     "pcamd_abi_version",
     "pcamd_last_error",
     "pcamd_quant_block",
+    "pcamd_quant_block_dual",
     "pcamd_quant_channel",
     "pcamd_quant_tensor",
     "pcamd_bmm_scaled",
@@ -57,6 +58,10 @@ def _declare(lib: ctypes.CDLL) -> None:
     quant_head = [_ptr, _int, _i64, _i64, _i64, _i64, _i64, _i64, _ptr, _int, _i64, _i64, _i64]
     lib.pcamd_quant_block.restype = _int
     lib.pcamd_quant_block.argtypes = quant_head + [_ptr, _i64, _i64, _i64, _i64, _i64, _flt, _flt, _ptr]
+    lib.pcamd_quant_block_dual.restype = _int
+    lib.pcamd_quant_block_dual.argtypes = (
+        [_ptr, _int, _i64, _i64, _i64, _i64, _i64, _i64, _ptr, _ptr, _int, _i64, _i64, _i64]
+        + [_ptr, _i64, _i64, _i64] * 2 + [_i64, _flt, _flt, _ptr])
     lib.pcamd_quant_channel.restype = _int
     lib.pcamd_quant_channel.argtypes = quant_head + [_ptr, _i64, _i64, _int, _flt, _flt, _ptr]
     lib.pcamd_quant_tensor.restype = _int

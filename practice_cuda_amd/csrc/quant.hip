@@ -20,6 +20,9 @@
 //   quant_colgroup_kernel  row-contiguous input with column groups
 //                       (block_n = 1, 16 <= block_m <= 256): one 128-column
 //                       strip of one row group per workgroup, held in registers.
+//   quant_dual_kernel   1 x 128 and 128 x 1 groups of one tensor from a
+//                       single read: one 128 x 128 block per workgroup,
+//                       row maxima by DPP, column maxima as above.
 //   quant_cols_kernel   whole columns (channel_axis = -1, two passes over the
 //                       strip), and column groups on grids too large for the
 //                       column-group kernel's 3-D grid.
@@ -649,6 +652,106 @@ __global__ __launch_bounds__(kThreads) void quant_colgroup_kernel(ColArgs a) {
 }
 
 // ===========================================================================
+// dual block quantization: 1 x 128 groups along n and 128 x 1 groups along m
+// of one row-contiguous tensor from a single read
+// ===========================================================================
+struct DualArgs {
+  const char* x;
+  uint8_t* yr;            // fp8 output of the 1 x 128 groups
+  uint8_t* yc;            // fp8 output of the 128 x 1 groups (same strides as yr)
+  float* sr;              // row-group scales [b, row, strip]
+  float* sc;              // column-group scales [b, row group, col]
+  int64_t m, n;
+  int64_t sxb, sxm, syb, sym;
+  int64_t srb, srm, srn, scb, scm, scn;
+  float fp8_max, eps;
+};
+
+// Grid (128-column strips, 128-row groups, batch), 256 threads. Lane t holds
+// columns 8 (t % 16) .. + 7 of rows t / 16 + 16 p (p < 8) of the 128 x 128
+// block, loaded up front. Each row's 128 columns sit in one aligned 16-lane
+// row of the wave (DPP max); column maxima meet as in quant_colgroup_kernel
+// (lane shuffles, then LDS across the waves). The results are those of the
+// 1 x 128 and 128 x 1 quantizers run separately. FULL: m and n are multiples
+// of 128, so no bounds checks.
+template <int DT, int FMT, bool NTS, bool FULL>
+__global__ __launch_bounds__(kThreads) void quant_dual_kernel(DualArgs a) {
+  constexpr int EB = elem_bytes<DT>();
+  constexpr int CPT = 8, WAVES = kThreads / 64;
+  __shared__ float part[WAVES][128];
+  __shared__ float qsv[128];
+  const int t = threadIdx.x;
+  const int lc = t & 15, rs = t >> 4;
+  const int64_t b = blockIdx.z, g = blockIdx.y, strip = blockIdx.x;
+  const int64_t col = strip * 128 + lc * 8;
+  const int64_t r0 = g * 128;
+  const char* xb = a.x + b * a.sxb * EB;
+  Chunk<DT> raw[CPT];
+#pragma unroll
+  for (int p = 0; p < CPT; ++p) {
+    const int64_t r = r0 + p * 16 + rs;
+    if (FULL || (r < a.m && col < a.n)) load_chunk<DT>(raw[p], xb + (r * a.sxm + col) * EB);
+    else zero_chunk<DT>(raw[p]);
+  }
+  // 1 x 128: one group per row of the strip
+  float rq[CPT];
+#pragma unroll
+  for (int p = 0; p < CPT; ++p) {
+    const Scales s = block_scales(group_max<16>(chunk_amax<DT>(raw[p])), a.fp8_max, a.eps);
+    rq[p] = s.qs;
+    const int64_t r = r0 + p * 16 + rs;
+    if (lc == 0 && (FULL || r < a.m)) a.sr[b * a.srb + r * a.srm + strip * a.srn] = s.ds;
+  }
+  // 128 x 1: one group per column of the strip
+  float cmax[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+  for (int p = 0; p < CPT; ++p) {
+    float v[8];
+    unpack_chunk<DT>(raw[p], v);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) cmax[i] = fmaxf(cmax[i], fabsf(v[i]));
+  }
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    cmax[i] = fmaxf(cmax[i], __shfl_xor(cmax[i], 16));
+    cmax[i] = fmaxf(cmax[i], __shfl_xor(cmax[i], 32));
+  }
+  if ((t & 63) < 16) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) part[t >> 6][lc * 8 + i] = cmax[i];
+  }
+  __syncthreads();
+  if (t < 128) {
+    float mx = part[0][t];
+#pragma unroll
+    for (int w = 1; w < WAVES; ++w) mx = fmaxf(mx, part[w][t]);
+    const Scales sc = block_scales(mx, a.fp8_max, a.eps);
+    qsv[t] = sc.qs;
+    const int64_t c = strip * 128 + t;
+    if (FULL || c < a.n) a.sc[b * a.scb + g * a.scm + c * a.scn] = sc.ds;
+  }
+  __syncthreads();
+  float qc[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) qc[i] = qsv[lc * 8 + i];
+  uint8_t* yrb = a.yr + b * a.syb;
+  uint8_t* ycb = a.yc + b * a.syb;
+#pragma unroll
+  for (int p = 0; p < CPT; ++p) {
+    const int64_t r = r0 + p * 16 + rs;
+    if (FULL || (r < a.m && col < a.n)) {
+      store8<DT, NTS>(yrb + r * a.sym + col, quant_chunk<DT, FMT>(raw[p], rq[p], a.fp8_max));
+      float v[8];
+      unpack_chunk<DT>(raw[p], v);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) v[i] = clamp_sym(v[i] * qc[i], a.fp8_max);
+      store8<DT, NTS>(ycb + r * a.sym + col,
+                      make_uint2(pack4<FMT>(v[0], v[1], v[2], v[3]), pack4<FMT>(v[4], v[5], v[6], v[7])));
+    }
+  }
+}
+
+// ===========================================================================
 // host dispatch helpers
 // ===========================================================================
 inline int grid_for(int64_t units, int64_t per_block = 1, int64_t cap = 1 << 20) {
@@ -800,6 +903,21 @@ struct LaunchColGroups {
 };
 
 template <int DT, int FMT>
+struct LaunchDual {
+  template <bool NTS>
+  static int go(const DualArgs& a, int64_t batch, hipStream_t st) {
+    const dim3 grid(static_cast<uint32_t>((a.n + 127) / 128), static_cast<uint32_t>((a.m + 127) / 128),
+                    static_cast<uint32_t>(batch));
+    if (a.m % 128 == 0 && a.n % 128 == 0) quant_dual_kernel<DT, FMT, NTS, true><<<grid, kThreads, 0, st>>>(a);
+    else quant_dual_kernel<DT, FMT, NTS, false><<<grid, kThreads, 0, st>>>(a);
+    return check_launch("quant_dual_kernel");
+  }
+  static int run(const DualArgs& a, int64_t batch, hipStream_t st) {
+    return nt_stores() ? go<true>(a, batch, st) : go<false>(a, batch, st);
+  }
+};
+
+template <int DT, int FMT>
 struct LaunchCols {
   static int run(const ColArgs& a, bool channel, hipStream_t st) {
     const int grid = grid_for(a.units);
@@ -945,6 +1063,41 @@ extern "C" int pcamd_quant_block(const void* x, int x_dtype, int64_t batch, int6
   a.ssb = ssb; a.ssm = ssm; a.ssn = ssn; a.bm = block_m; a.bn = block_n; a.mb = mb; a.nb = nb;
   a.units = batch * mb * nb; a.fp8_max = fp8_max; a.eps = eps;
   return dispatch_dt_fmt<LaunchGeneric>(x_dtype, y_dtype, a, 0, st);
+}
+
+extern "C" int pcamd_quant_block_dual(const void* x, int x_dtype, int64_t batch, int64_t m, int64_t n,
+                                      int64_t sxb, int64_t sxm, int64_t sxn, void* y_row, void* y_col,
+                                      int y_dtype, int64_t syb, int64_t sym, int64_t syn,
+                                      float* scale_row, int64_t srb, int64_t srm, int64_t srn,
+                                      float* scale_col, int64_t scb, int64_t scm, int64_t scn,
+                                      int64_t block, float fp8_max, float eps, void* stream) {
+  clear_error();
+  int rc = validate_common(x, x_dtype, batch, m, n, y_row, y_dtype, scale_row, fp8_max);
+  if (rc) return rc;
+  if (batch * m * n > 0 && (!y_col || !scale_col)) return set_error(PCAMD_ERR_INVALID, "null pointer");
+  if (batch * m * n > 0 && (y_row == y_col || scale_row == scale_col))
+    return set_error(PCAMD_ERR_INVALID, "the two outputs (and the two scale tensors) must not alias");
+  if (!is_pow2(block))
+    return set_error(PCAMD_ERR_INVALID, "block size must be a power of two, got %lld", (long long)block);
+  if (batch == 0 || m == 0 || n == 0) return PCAMD_OK;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const bool fast = row_fast_ok(x, x_dtype, y_row, n, sxb, sxm, sxn, syb, sym, syn) && aligned(y_col, 8);
+  if (fast && block == 128 && batch <= 65535 && (m + 127) / 128 <= 65535 && (n + 127) / 128 <= INT32_MAX) {
+    DualArgs a{};
+    a.x = static_cast<const char*>(x);
+    a.yr = static_cast<uint8_t*>(y_row); a.yc = static_cast<uint8_t*>(y_col);
+    a.sr = scale_row; a.sc = scale_col;
+    a.m = m; a.n = n; a.sxb = sxb; a.sxm = sxm; a.syb = syb; a.sym = sym;
+    a.srb = srb; a.srm = srm; a.srn = srn; a.scb = scb; a.scm = scm; a.scn = scn;
+    a.fp8_max = fp8_max; a.eps = eps;
+    return dispatch_dt_fmt<LaunchDual>(x_dtype, y_dtype, a, batch, st);
+  }
+  // other layouts and block sizes: the two quantizers one after the other
+  rc = pcamd_quant_block(x, x_dtype, batch, m, n, sxb, sxm, sxn, y_row, y_dtype, syb, sym, syn, scale_row,
+                         srb, srm, srn, 1, block, fp8_max, eps, stream);
+  if (rc) return rc;
+  return pcamd_quant_block(x, x_dtype, batch, m, n, sxb, sxm, sxn, y_col, y_dtype, syb, sym, syn, scale_col,
+                           scb, scm, scn, block, 1, fp8_max, eps, stream);
 }
 
 extern "C" int pcamd_quant_channel(const void* x, int x_dtype, int64_t batch, int64_t m, int64_t n,

@@ -75,6 +75,57 @@ def hip_per_block_quant(
     )
 
 
+def hip_per_block_quant_dual(
+    x: torch.Tensor,
+    *,
+    block: int = 128,
+    fp8_dtype: torch.dtype = torch.float8_e4m3fn,
+    eps: float = 1e-12,
+) -> tuple[QuantResult, QuantResult]:
+    """``(hip_per_block_quant(x, block_m=1, block_n=block), hip_per_block_quant(x,
+    block_m=block, block_n=1))`` from one read of x.
+
+    The block-scaled training recipe needs both quantizations of the
+    activations and of the output gradient: 1 x block groups along the last
+    dim for the forward / dgrad GEMMs, block x 1 groups along the rows for
+    wgrad. The results are bit-identical to the two separate calls.
+    """
+    if x.ndim not in (2, 3):
+        raise ValueError(f"per-block quant expects a 2D or 3D tensor, got {tuple(x.shape)}")
+    if not C.is_power_of_two(block):
+        raise ValueError(f"per-block quant currently requires power-of-two block sizes; got block={block}")
+    C.check_quant_input(x, fp8_dtype, "per-block quant")
+    _lib.require_gpu_tensor(x, "x")
+
+    out_row = torch.empty_like(x, dtype=fp8_dtype, memory_format=torch.preserve_format)
+    out_col = torch.empty_like(out_row)
+    batch, m, n, xs, ys = C.dims3(x, out_row)
+    if tuple(out_col.stride()) != tuple(out_row.stride()):
+        out_col = torch.empty_strided(out_row.shape, out_row.stride(), dtype=fp8_dtype, device=x.device)
+    s_row = torch.empty((batch, m, -(-n // block)), device=x.device, dtype=torch.float32)
+    s_col = torch.empty((batch, -(-m // block), n), device=x.device, dtype=torch.float32)
+
+    L = _lib.lib()
+    with torch.cuda.device(x.device):
+        rc = L.pcamd_quant_block_dual(
+            _lib.ptr(x), _lib.dtype_code(x.dtype), batch, m, n, *xs,
+            _lib.ptr(out_row), _lib.ptr(out_col), _lib.dtype_code(fp8_dtype), *ys,
+            _lib.ptr(s_row), *s_row.stride(), _lib.ptr(s_col), *s_col.stride(),
+            block, float(torch.finfo(fp8_dtype).max), float(eps), _lib.stream_of(x))
+    _lib.check(rc, "pcamd_quant_block_dual")
+
+    def result(q, s, bm, bn):
+        return QuantResult(
+            tensor=q,
+            dequant_scale=s.squeeze(0) if x.ndim == 2 else s,
+            impl="hip_per_block",
+            granularity="block",
+            meta={"logical_shape": tuple(x.shape), "fp8_dtype": str(fp8_dtype), "block_m": bm, "block_n": bn},
+        )
+
+    return result(out_row, s_row, 1, block), result(out_col, s_col, block, 1)
+
+
 def _validate_scale(value: QuantResult, *, expected_shape, expected_block_m, expected_block_n,
                     operand: str) -> None:
     scale = value.dequant_scale

@@ -8,8 +8,11 @@ recipe the reference leaves unfinished (``modules/per_block.py:13-67``):
 
 * forward  ``Y = X W^T (+ bias)``: X quantized 1x128 along K, W 128x128;
 * dgrad    ``dX = dY W``: dY quantized 1x128 along N, W reused from forward;
-* wgrad    ``dW = dY^T X``: dY and X re-quantized 128x1 (blocks of 128 along
-  M, the reduction dimension of this GEMM) from their high-precision values;
+* wgrad    ``dW = dY^T X``: dY and X quantized 128x1 (blocks of 128 along
+  M, the reduction dimension of this GEMM) from their high-precision values,
+  each in the same pass as its 1x128 quantization (``pcamd_quant_block_dual``:
+  one read of X in forward, one of dY in backward; the 128x1 fp8 X is what
+  forward saves);
 * dbias    ``dY.sum(1)``.
 
 Every GEMM is ``pcamd::block_scaled_bmm``, a ``torch.library`` custom op over
@@ -30,7 +33,7 @@ import torch.nn as nn
 
 from . import _lib
 from .impls import _common as C
-from .impls.hip_per_block import hip_per_block_quant
+from .impls.hip_per_block import hip_per_block_quant, hip_per_block_quant_dual
 from .impls.hip_per_tensor import quant_tensor_raw
 
 _FP8 = (torch.float8_e4m3fn, torch.float8_e5m2)
@@ -129,6 +132,23 @@ def _(x, block_m, block_n, fp8_dtype, eps):
             x.new_empty((b, -(-m // block_m), -(-n // block_n)), dtype=torch.float32))
 
 
+@torch.library.custom_op("pcamd::quant_block_dual", mutates_args=())
+def quant_block_dual(x: torch.Tensor, block: int, fp8_dtype: torch.dtype,
+                     eps: float) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
+    """``quant_block(x, 1, block)`` and ``quant_block(x, block, 1)`` from one read
+    of x: (fp8 1 x block, its scales [B, M, ceil(N/block)], fp8 block x 1, its
+    scales [B, ceil(M/block), N])."""
+    r, c = hip_per_block_quant_dual(x, block=block, fp8_dtype=fp8_dtype, eps=eps)
+    return r.tensor, r.dequant_scale, c.tensor, c.dequant_scale
+
+
+@quant_block_dual.register_fake
+def _(x, block, fp8_dtype, eps):
+    b, m, n = x.shape
+    return (torch.empty_like(x, dtype=fp8_dtype), x.new_empty((b, m, -(-n // block)), dtype=torch.float32),
+            torch.empty_like(x, dtype=fp8_dtype), x.new_empty((b, -(-m // block), n), dtype=torch.float32))
+
+
 @torch.library.custom_op("pcamd::quant_tensor", mutates_args=())
 def quant_tensor(x: torch.Tensor, fp8_dtype: torch.dtype, eps: float) -> tuple[torch.Tensor, torch.Tensor]:
     """(fp8 tensor like x, fp32 dequant scale of shape [1])."""
@@ -187,9 +207,14 @@ class _Float8BlockBMMLinearFunction(torch.autograd.Function):
             qw, sw = torch.ops.pcamd.quant_tensor(weight, f8, eps)
             ctx.save_for_backward(qx, sx, qw, sw)
             return torch.ops.pcamd.tensor_scaled_bmm(qx, qw.transpose(-2, -1), sx * sw, bias_k, input.dtype)
-        qx, sx = torch.ops.pcamd.quant_block(input, 1, blk, f8, eps)      # [B,M,K], [B,M,K/128]
+        if ctx.needs_input_grad[1]:
+            # wgrad needs X quantized in 128-row blocks too: both from one read
+            qx, sx, qxm, sxm = torch.ops.pcamd.quant_block_dual(input, blk, f8, eps)
+        else:
+            qx, sx = torch.ops.pcamd.quant_block(input, 1, blk, f8, eps)  # [B,M,K], [B,M,K/128]
+            qxm = sxm = None
         qw, sw = torch.ops.pcamd.quant_block(weight, blk, blk, f8, eps)   # [B,N,K], [B,N/128,K/128]
-        ctx.save_for_backward(input, qw, sw)
+        ctx.save_for_backward(qxm, sxm, qw, sw)
         # B = W^T: [B,K,N] contiguous along K; its scales [B,K/128,N/128]
         return _block_gemm(qx, sx, qw.transpose(-2, -1), sw.transpose(-2, -1), bias_k, 1, blk, input.dtype, blk)
 
@@ -207,15 +232,20 @@ class _Float8BlockBMMLinearFunction(torch.autograd.Function):
             if ctx.needs_input_grad[1]:
                 grad_weight = torch.ops.pcamd.tensor_scaled_bmm(qdy.transpose(-2, -1), qx, sdy * sx, None, dy.dtype)
         else:
-            input, qw, sw = ctx.saved_tensors
-            if ctx.needs_input_grad[0]:
-                # dX = dY W: A = dY [B,M,N] 1x128 along N; B = W [B,N,K] (N = reduction)
-                qdy, sdy = torch.ops.pcamd.quant_block(dy, 1, blk, f8, eps)
-                grad_input = _block_gemm(qdy, sdy, qw, sw, None, 1, blk, dy.dtype, blk)
-            if ctx.needs_input_grad[1]:
-                # dW = dY^T X: both re-quantized with 128-row blocks along M
+            qxm, sxm, qw, sw = ctx.saved_tensors
+            need_dx, need_dw = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
+            if need_dx and need_dw:
+                # dY quantized 1x128 along N (dgrad) and in 128-row blocks (wgrad) from one read
+                qdy, sdy, qdt, sdt = torch.ops.pcamd.quant_block_dual(dy, blk, f8, eps)
+            elif need_dx:
+                qdy, sdy = torch.ops.pcamd.quant_block(dy, 1, blk, f8, eps)      # [B,M,N], [B,M,N/128]
+            elif need_dw:
                 qdt, sdt = torch.ops.pcamd.quant_block(dy, blk, 1, f8, eps)      # [B,M,N], [B,M/128,N]
-                qxm, sxm = torch.ops.pcamd.quant_block(input, blk, 1, f8, eps)   # [B,M,K], [B,M/128,K]
+            if need_dx:
+                # dX = dY W: A = dY [B,M,N] 1x128 along N; B = W [B,N,K] (N = reduction)
+                grad_input = _block_gemm(qdy, sdy, qw, sw, None, 1, blk, dy.dtype, blk)
+            if need_dw:
+                # dW = dY^T X: dY and X (quantized in forward) in 128-row blocks along M
                 grad_weight = _block_gemm(qdt.transpose(-2, -1), sdt.transpose(-2, -1), qxm, sxm, None,
                                           1, 1, dy.dtype, blk)
         if ctx.has_bias and ctx.needs_input_grad[2]:
@@ -323,4 +353,4 @@ def convert_to_float8_bmm_training(module: nn.Module,
 
 
 __all__ = ["BMMLinear", "Float8BMMLinear", "Float8BlockBMMLinearConfig", "convert_to_float8_bmm_training",
-           "block_scaled_bmm", "tensor_scaled_bmm", "quant_block", "quant_tensor"]
+           "block_scaled_bmm", "tensor_scaled_bmm", "quant_block", "quant_block_dual", "quant_tensor"]

@@ -223,6 +223,81 @@ def test_config3_full_size(dev):
 
 
 # ---------------------------------------------------------------------------
+# dual 1 x 128 + 128 x 1 quantization (one read, both outputs)
+# ---------------------------------------------------------------------------
+DUAL_CASES = [
+    ((256, 384), "bf16", 128, "e4m3", None),          # whole blocks
+    ((3, 256, 640), "f16", 128, "e5m2", None),        # batch
+    ((200, 520), "bf16", 128, "e4m3", None),          # ragged rows, partial last strip
+    ((2, 130, 136), "f32", 128, "e4m3", None),        # fp32 input, ragged both ways
+    ((96, 1000), "bf16", 128, "e4m3", "outliers"),
+    ((45, 77), "bf16", 128, "e4m3", None),            # n % 8 != 0: the two quantizers in turn
+    ((256, 256), "bf16", 64, "e4m3", None),           # other block size: the two quantizers in turn
+    ((384, 256), "bf16", 128, "e4m3", "transposed"),  # column-major input: the two quantizers in turn
+    ((256, 384), "bf16", 128, "e4m3", "zero_rows"),
+    ((2, 256, 384), "bf16", 128, "e4m3", "padded"),   # row pitch 640 (a column slice)
+]
+
+
+@pytest.mark.parametrize("shape,dtype,block,fmt,kind", DUAL_CASES)
+def test_dual_matches_oracle(dev, shape, dtype, block, fmt, kind):
+    from practice_cuda_amd.impls.hip_per_block import hip_per_block_quant_dual
+    x = make_input(shape, dtype, seed=sum(shape) + block, outliers=0.01 if kind == "outliers" else 0.0)
+    if kind == "zero_rows":
+        x[5:37] = 0
+        x[:, 129:257] = 0
+    xd = x.to(dev)
+    if kind == "transposed":
+        x = x.t().contiguous().t()        # same values, column-major strides
+        xd = xd.t().contiguous().t()
+    if kind == "padded":
+        wide = torch.zeros(*shape[:-1], 640, dtype=x.dtype, device=dev)
+        wide[..., :shape[-1]] = xd
+        xd = wide[..., :shape[-1]]
+    print(f"dual shape={shape} dtype={dtype} block={block} fmt={fmt} kind={kind}", flush=True)
+    r_row, r_col = hip_per_block_quant_dual(xd, block=block, fp8_dtype=FMT[fmt])
+    q1, s1 = O.quant_block(x, 1, block, fmt=fmt)
+    q2, s2 = O.quant_block(x, block, 1, fmt=fmt)
+    assert r_row.meta["block_m"] == 1 and r_row.meta["block_n"] == block
+    assert r_col.meta["block_m"] == block and r_col.meta["block_n"] == 1
+    assert_same(r_row, q1, s1, "dual 1 x block")
+    assert_same(r_col, q2, s2, "dual block x 1")
+    # and the same bits as the two separate entry points
+    for r, bm, bn in ((r_row, 1, block), (r_col, block, 1)):
+        one = hip_per_block_quant(xd, block_m=bm, block_n=bn, fp8_dtype=FMT[fmt])
+        assert np.array_equal(qbits(r.tensor), qbits(one.tensor))
+        assert np.array_equal(sbits(r.dequant_scale), sbits(one.dequant_scale))
+        assert r.dequant_scale.shape == one.dequant_scale.shape
+
+
+def test_dual_full_size(dev):
+    """Both quantizations of the config-1 input shape (bf16 [4096, 7168],
+    N(0,1) with 0.1% outliers x50) from one kernel, bit-exact."""
+    from practice_cuda_amd.impls.hip_per_block import hip_per_block_quant_dual
+    g = torch.Generator().manual_seed(2)
+    x = torch.randn(4096, 7168, generator=g)
+    m = torch.rand(4096, 7168, generator=g) < 0.001
+    x[m] *= 50
+    x = x.bfloat16()
+    r_row, r_col = hip_per_block_quant_dual(x.to(dev), block=128)
+    q1, s1 = O.quant_block(x, 1, 128, threads=8)
+    assert_same(r_row, q1, s1, "dual 1x128 full size")
+    q2, s2 = O.quant_block(x, 128, 1, threads=8)
+    assert_same(r_col, q2, s2, "dual 128x1 full size")
+
+
+def test_dual_rejects_aliased_outputs(dev):
+    x = torch.randn(128, 128, device=dev).bfloat16()
+    y = torch.empty(128, 128, device=dev, dtype=torch.float8_e4m3fn)
+    s1 = torch.empty(128, 1, device=dev)
+    s2 = torch.empty(1, 128, device=dev)
+    rc = _lib.lib().pcamd_quant_block_dual(
+        _lib.ptr(x), _lib.BF16, 1, 128, 128, 0, 128, 1, _lib.ptr(y), _lib.ptr(y), _lib.E4M3FN,
+        0, 128, 1, _lib.ptr(s1), 0, 1, 1, _lib.ptr(s2), 0, 128, 1, 128, 448.0, 1e-12, _lib.stream_of(x))
+    assert rc == -1 and b"alias" in _lib.lib().pcamd_last_error()
+
+
+# ---------------------------------------------------------------------------
 # per-channel
 # ---------------------------------------------------------------------------
 CHANNEL_CASES = [
