@@ -89,20 +89,29 @@ PCAMD_DEV int swz_k(int r) { return (((r >> 1) & 1) * 5) ^ ((r >> 2) & 1); }
 // rb + (l >> 3) and LDS slot l & 7, which holds global chunk
 // (l & 7) ^ swz_k(r). rb is a multiple of 8 and swz_k reads only bits 1-2 of
 // r, so swz_k(r) = swz_k(l >> 3) and one lane offset serves every instruction.
+//
+// The row part of the offset (tile origin, instruction, lane) is fixed for the
+// tile and kept per instruction in VGPRs; the K step's byte offset k0 goes in
+// the instruction's SGPR offset, so no VALU work is issued per load. Rows past
+// the matrix are out of range through the VGPR part alone; for rows inside
+// it, row * ld + k0 + 127 stays below the row's end (k0 < K <= ld).
 template <int ROWS>
 struct KMajorLoader {
   static constexpr int PER_WAVE = ROWS / WAVES;
   static constexpr int INSTS = PER_WAVE / 8;
-  uint32_t voff;
-  PCAMD_DEV KMajorLoader(uint32_t ld, int lane, int /*wave*/)
-      : voff((lane >> 3) * ld + (((lane & 7) ^ swz_k(lane >> 3)) << 4)) {}
-  PCAMD_DEV void issue(v4i rs, uint8_t* tile, uint32_t row0, uint32_t ld, uint32_t k0, int wave) const {
+  uint32_t voff[INSTS];
+  PCAMD_DEV KMajorLoader(uint32_t ld, int lane, int wave, uint32_t row0) {
+    const uint32_t lp = (lane >> 3) * ld + (((lane & 7) ^ swz_k(lane >> 3)) << 4);
+#pragma unroll
+    for (int i = 0; i < INSTS; ++i) voff[i] = (row0 + wave * PER_WAVE + i * 8) * ld + lp;
+  }
+  // tile_lds: LDS byte address of the tile
+  PCAMD_DEV void issue(v4i rs, uint32_t tile_lds, uint32_t k0, int wave) const {
 #pragma unroll
     for (int i = 0; i < INSTS; ++i) {
-      const int rb = wave * PER_WAVE + i * 8;
-      uint32_t u = __builtin_amdgcn_readfirstlane((row0 + rb) * ld + k0);
-      asm volatile("" : "+s"(u));
-      lds_dma16(rs, lds_addr(tile + rb * BK), voff + u);
+      const uint32_t lds = tile_lds + (wave * PER_WAVE + i * 8) * BK;
+      asm volatile("buffer_load_dwordx4 %0, %1, %2 offen lds" ::"v"(voff[i]), "s"(rs), "s"(k0), "{m0}"(lds)
+                   : "memory");
     }
   }
 };
@@ -251,13 +260,20 @@ __global__ __launch_bounds__(NT, 1) void bmm_wide_kernel(FastArgs a) {
   const v4i rsb = make_rsrc(a.b + bidx * a.sbb, a.b_extent);
   using LA = typename std::conditional<A_K, KMajorLoader<BM>, MNMajorLoader<BM>>::type;
   using LB = typename std::conditional<B_K, KMajorLoader<BN>, MNMajorLoader<BN>>::type;
-  const LA load_a(a.lda, lane, wave);
-  const LB load_b(a.ldb, lane, wave);
+  auto make_loader = [&](auto is_k, uint32_t ld, uint32_t origin) {
+    if constexpr (decltype(is_k)::value) return KMajorLoader<BM>(ld, lane, wave, origin);
+    else return MNMajorLoader<BM>(ld, lane, wave);
+  };
+  const LA load_a = make_loader(std::integral_constant<bool, A_K>{}, a.lda, m0);
+  const LB load_b = make_loader(std::integral_constant<bool, B_K>{}, a.ldb, n0);
 
   auto issue = [&](int ks, uint8_t* stage) {
-    const uint32_t k0 = ks * BK;
-    load_a.issue(rsa, stage, m0, a.lda, k0, wave);
-    load_b.issue(rsb, stage + A_BYTES, n0, a.ldb, k0, wave);
+    const uint32_t k0 = __builtin_amdgcn_readfirstlane(ks * BK);
+    const uint32_t base = lds_addr(stage);  // one generic -> LDS conversion per step
+    if constexpr (A_K) load_a.issue(rsa, base, k0, wave);
+    else load_a.issue(rsa, base, m0, a.lda, k0, wave);
+    if constexpr (B_K) load_b.issue(rsb, base + A_BYTES, k0, wave);
+    else load_b.issue(rsb, base + A_BYTES, n0, a.ldb, k0, wave);
   };
   auto afrag = [&](const uint8_t* stage, int i) -> v8i {
     if constexpr (A_K) return frag_k(stage, wm * 64 + i * 16 + lr, lg);
