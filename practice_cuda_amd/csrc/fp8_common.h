@@ -55,11 +55,18 @@ struct Chunk {
   uint4 r[DT == kF32 ? 2 : 1];
 };
 
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+
+// Input chunks are read once: non-temporal loads.
 template <int DT>
 PCAMD_DEV void load_chunk(Chunk<DT>& c, const void* p) {
-  const uint4* q = static_cast<const uint4*>(p);
-  c.r[0] = q[0];
-  if constexpr (DT == kF32) c.r[1] = q[1];
+  const u32x4_t* q = static_cast<const u32x4_t*>(p);
+  const u32x4_t a = __builtin_nontemporal_load(q);
+  c.r[0] = make_uint4(a.x, a.y, a.z, a.w);
+  if constexpr (DT == kF32) {
+    const u32x4_t b = __builtin_nontemporal_load(q + 1);
+    c.r[1] = make_uint4(b.x, b.y, b.z, b.w);
+  }
 }
 
 template <int DT>
