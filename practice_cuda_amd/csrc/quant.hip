@@ -12,8 +12,8 @@
 //   quant_waverow_kernel   per-channel along rows (channel_axis = -2), rows
 //                       of up to 2048 elements: one wave per row.
 //   quant_rowblock_kernel  per-channel along rows, 2048 to 16384 elements: one
-//                       workgroup per row sized to two chunks per lane, DPP +
-//                       one LDS max.
+//                       workgroup per row sized to two (rows up to 4096
+//                       elements) or four chunks per lane, DPP + one LDS max.
 //   quant_tile_kernel   one workgroup per block_m x block_n block held in
 //                       registers (e.g. 128 x 128 = 8 chunks per thread);
 //                       wave DPP max, then an LDS max across the 4 waves.
@@ -170,9 +170,9 @@ __global__ __launch_bounds__(kThreads) void quant_waverow_kernel(RowArgs a) {
   }
 }
 
-// Per-channel along the row: one workgroup per row, thread t owning chunks
-// t, t + 256, ... (CPT of them, 256 * CPT >= chunks). Wave DPP max, then one
-// LDS exchange across the four waves.
+// Per-channel along the row: one workgroup of nt threads per row, thread t
+// owning chunks t, t + nt, ... (CPT of them, nt * CPT >= chunks). Wave DPP
+// max, then one LDS exchange across the waves.
 // GRID2: grid (rows, batch), so the row and batch come from the workgroup
 // index with no division ahead of the loads; otherwise a 1-D grid of
 // batch * rows.
@@ -836,14 +836,15 @@ struct LaunchRowBlock {
   template <bool NTS>
   static int pick(const RowArgs& a, hipStream_t st) {
     // Rows shorter than 2048 elements: one wave per row. Longer (up to 16384):
-    // one workgroup per row, two chunks per lane, the workgroup size the
-    // smallest multiple of 64 that covers the row. A sweep over 2048-16384
-    // elements: 1-5 % faster than 256-thread workgroups with 2-8 chunks per
-    // lane, and than one wave per row at 2048 (7168: 448 threads, no idle
-    // chunk slot, 68.6 -> 66.6 us on the config-2 tensor).
+    // one workgroup per row, the workgroup size the smallest multiple of 64
+    // that covers the row with two chunks per lane up to 4096 elements and
+    // four beyond. A sweep over 2048-16384 elements (non-temporal loads, 2, 3
+    // or 4 chunks per lane): four per lane 2-6 % faster from 5120 elements
+    // on, equal at 4096 and 8192, two per lane 1 % faster at 2048 (7168: 256
+    // threads, 63.4 -> 61.5 us on the config-2 tensor).
     if (a.chunks < 256) return wave<4, NTS>(a, st);
-    const int threads = ((a.chunks + 1) / 2 + 63) / 64 * 64;  // <= 1024: chunks <= 2048
-    return go<2, NTS>(a, threads, st);
+    if (a.chunks <= 512) return go<2, NTS>(a, ((a.chunks + 1) / 2 + 63) / 64 * 64, st);
+    return go<4, NTS>(a, ((a.chunks + 3) / 4 + 63) / 64 * 64, st);  // <= 512 threads: chunks <= 2048
   }
   static int run(const RowArgs& a, hipStream_t st) { return nt_stores() ? pick<true>(a, st) : pick<false>(a, st); }
 };
