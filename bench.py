@@ -352,7 +352,40 @@ def cpu_baseline(torch, x_cpu):
     return {"value": nbytes / t / 1e9, "unit": "GB/s", "cores": threads, "kind": "port",
             "sample": f"bf16 [{m},{n}] (the full workload tensor), "
                       f"median of 5 runs of oracle/fp8_oracle.c per-channel quant, "
-                      f"{threads} OpenMP threads, {t * 1e3:.1f} ms/run"}
+                      f"{threads} OpenMP threads, {t * 1e3:.1f} ms/run",
+            "torch_eager": torch_eager_baseline(torch, sample, threads)}
+
+
+def torch_channel_quant(torch, x, fp8_max=448.0, eps=1e-12):
+    """The reference's PyTorch form of the per-row quantizer
+    (kernels/quant/per_channel.py:9-29, channel_axis=-2): fp32 math, amax
+    per row, s = max(amax, eps), q = fp8(clamp(x * (fp8_max / s))), scale
+    s / fp8_max."""
+    xf = x.float()
+    s = xf.abs().amax(dim=-1, keepdim=True).clamp(min=eps)
+    q = (xf * (fp8_max / s)).clamp(-fp8_max, fp8_max).to(torch.float8_e4m3fn)
+    return q, (s / fp8_max).squeeze(-1)
+
+
+def torch_eager_baseline(torch, sample, threads):
+    """The same workload through eager PyTorch on the host cores (the
+    reference's CPU path), checked against the oracle on the first rows."""
+    from oracle import oracle as O
+    q_ref, s_ref = O.quant_channel(sample[:64], -2, threads=threads)
+    torch.set_num_threads(threads)  # after the oracle call: both set the process's OpenMP thread count
+    q, s = torch_channel_quant(torch, sample[:64])
+    same = bool((q.view(torch.uint8).numpy() == q_ref).all() and (s.numpy().view("uint32") == s_ref.view("uint32")).all())
+    times = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        torch_channel_quant(torch, sample)
+        times.append(time.perf_counter() - t0)
+    t = statistics.median(times)
+    m, n = sample.shape
+    return {"value": (m * n * 3 + m * 4) / t / 1e9, "unit": "GB/s", "threads": torch.get_num_threads(),
+            "matches_oracle": same,
+            "sample": f"bf16 [{m},{n}], median of 3 runs of the eager-PyTorch per-row quantizer "
+                      f"(fp32 math), {t * 1e3:.1f} ms/run"}
 
 
 def pmc_probe(torch, dev):
