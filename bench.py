@@ -11,9 +11,10 @@ timed with HIP events on the stream the kernels run on. Inputs are resident
 in HBM before the timed region starts.
 
 ``components`` reports the other BASELINE configs the same way (1x128 quant,
-128x128 quant, the block-scaled BMM of config 4 and the config-5 GEMM trio).
-``cpu_baseline`` times the CPU restatement of the same quantizer (oracle/,
-OpenMP over rows) on the host cores.
+128x128 quant, config 2's weight with one scale per column, the block-scaled
+BMM of config 4 and the config-5 GEMM trio). ``cpu_baseline`` times the CPU
+restatement of the same quantizer (oracle/, OpenMP over rows) on the host
+cores, and the reference's eager-PyTorch form of it.
 """
 from __future__ import annotations
 
@@ -143,6 +144,17 @@ def quant_channel_launcher(torch, L, xs, ys, ss):
     return launch
 
 
+def quant_columns_launcher(torch, L, xs, ys, ss):
+    def launch(i):
+        x, y, s = xs[i % len(xs)], ys[i % len(ys)], ss[i % len(ss)]
+        rc = L.lib().pcamd_quant_channel(
+            L.ptr(x), L.BF16, 1, x.shape[0], x.shape[1], 0, x.stride(0), 1,
+            L.ptr(y), L.E4M3FN, 0, y.stride(0), 1, L.ptr(s), 0, 1, -1, 448.0, 1e-12,
+            L.stream_of(x))
+        L.check(rc, "pcamd_quant_channel")
+    return launch
+
+
 def quant_block_launcher(torch, L, xs, ys, ss, bm, bn):
     def launch(i):
         x, y, s = xs[i % len(xs)], ys[i % len(ys)], ss[i % len(ss)]
@@ -194,6 +206,10 @@ def bench_quant(torch, name, x_cpu, kind, steps, warmup, nsets, dev, bm=1, bn=12
         ss = [torch.empty(m, dtype=torch.float32, device=dev) for _ in range(nsets)]
         launch = quant_channel_launcher(torch, L, xs, ys, ss)
         scale_bytes = m * 4
+    elif kind == "columns":
+        ss = [torch.empty(n, dtype=torch.float32, device=dev) for _ in range(nsets)]
+        launch = quant_columns_launcher(torch, L, xs, ys, ss)
+        scale_bytes = n * 4
     else:
         mb, nb = -(-m // bm), -(-n // bn)
         ss = [torch.empty(mb, nb, dtype=torch.float32, device=dev) for _ in range(nsets)]
@@ -473,6 +489,11 @@ def main():
             if not only or "config3" in only:
                 comps.append(bench_quant(torch, "config3_128x128_quant_4096x7168", make_config3(torch),
                                          "block", args.steps, args.warmup, 8, dev, 128, 128))
+            if not only or "columns" in only:
+                # config 2's weight with one scale per column (channel_axis=-1: the
+                # reference bench's default axis, and the per-channel BMM's B operand)
+                comps.append(bench_quant(torch, "config2_weight_per_column_quant_18432x7168", make_config2(torch),
+                                         "columns", args.steps, args.warmup, 4, dev))
             if not only or "config4" in only:
                 comps.append(bench_config4(torch, args.steps, args.warmup, dev))
             if not only or "config5" in only:

@@ -23,9 +23,12 @@
 //   quant_dual_kernel   1 x 128 and 128 x 1 groups of one tensor from a
 //                       single read: one 128 x 128 block per workgroup,
 //                       row maxima by DPP, column maxima as above.
-//   quant_cols_kernel   whole columns (channel_axis = -1, two passes over the
-//                       strip), and column groups on grids too large for the
-//                       column-group kernel's 3-D grid.
+//   colchan_*_kernel    whole columns of tall tensors (channel_axis = -1):
+//                       column maxima of 128-row slabs by atomic max into
+//                       the scale slots, then a quantize pass per slab.
+//   quant_cols_kernel   whole columns of up to 256 rows (channel_axis = -1,
+//                       two passes over the strip), and column groups on grids
+//                       too large for the column-group kernel's 3-D grid.
 //   quant_*_generic     any strides / block shape; one workgroup per block or
 //                       channel, two passes (second read served by L2).
 //   per-tensor          amax kernel (workgroup max + one atomic max on the
@@ -652,6 +655,117 @@ __global__ __launch_bounds__(kThreads) void quant_colgroup_kernel(ColArgs a) {
 }
 
 // ===========================================================================
+// per-column scales (channel_axis = -1) of tall tensors: column maxima over
+// 128-row slabs meet through atomic max in the scale slots, then a second
+// kernel quantizes each slab and a third turns the maxima into scales
+// ===========================================================================
+// scale[b, c] = 0 (the bit pattern the atomic maxima start from)
+__global__ __launch_bounds__(kThreads) void colchan_zero_kernel(ColArgs a) {
+  const int64_t i = int64_t(blockIdx.x) * kThreads + threadIdx.x;
+  if (i >= (a.units / a.strips) * a.n) return;  // units / strips = batch
+  const int64_t b = i / a.n, c = i - b * a.n;
+  reinterpret_cast<uint32_t*>(a.scale)[b * a.ssb + c * a.ssn] = 0u;
+}
+
+// Grid (128-column strips, 128-row slabs, batch), 256 threads: lane t takes
+// columns 8 (t % 16) .. + 7 of rows t / 16 + 16 p (p < 8) of its slab. The
+// slab's column maxima (lane shuffles, then LDS across the waves) go to the
+// scale slots by atomic max on the fp32 bit patterns (for non-negative
+// values their uint32 order is the float order).
+template <int DT>
+__global__ __launch_bounds__(kThreads) void colchan_amax_kernel(ColArgs a) {
+  constexpr int EB = elem_bytes<DT>();
+  constexpr int CPT = 8, WAVES = kThreads / 64;
+  __shared__ float part[WAVES][128];
+  const int t = threadIdx.x;
+  const int lc = t & 15, rs = t >> 4;
+  const int64_t b = blockIdx.z, strip = blockIdx.x;
+  const int64_t col = strip * 128 + lc * 8;
+  const int64_t r0 = int64_t(blockIdx.y) * 128;
+  const char* xb = a.x + b * a.sxb * EB;
+  Chunk<DT> raw[CPT];
+#pragma unroll
+  for (int p = 0; p < CPT; ++p) {
+    const int64_t r = r0 + p * 16 + rs;
+    if (r < a.m && col < a.n) load_chunk<DT>(raw[p], xb + (r * a.sxm + col) * EB);
+    else zero_chunk<DT>(raw[p]);
+  }
+  float cmax[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+  for (int p = 0; p < CPT; ++p) {
+    float v[8];
+    unpack_chunk<DT>(raw[p], v);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) cmax[i] = fmaxf(cmax[i], fabsf(v[i]));
+  }
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    cmax[i] = fmaxf(cmax[i], __shfl_xor(cmax[i], 16));
+    cmax[i] = fmaxf(cmax[i], __shfl_xor(cmax[i], 32));
+  }
+  if ((t & 63) < 16) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) part[t >> 6][lc * 8 + i] = cmax[i];
+  }
+  __syncthreads();
+  if (t < 128) {
+    float mx = part[0][t];
+#pragma unroll
+    for (int w = 1; w < WAVES; ++w) mx = fmaxf(mx, part[w][t]);
+    const int64_t c = strip * 128 + t;
+    if (c < a.n) atomicMax(reinterpret_cast<uint32_t*>(a.scale) + b * a.ssb + c * a.ssn, __float_as_uint(mx));
+  }
+}
+
+// Same grid: quantize the slab with the finished column maxima.
+template <int DT, int FMT, bool NTS>
+__global__ __launch_bounds__(kThreads) void colchan_apply_kernel(ColArgs a) {
+  constexpr int EB = elem_bytes<DT>();
+  constexpr int CPT = 8;
+  const int t = threadIdx.x;
+  const int lc = t & 15, rs = t >> 4;
+  const int64_t b = blockIdx.z, strip = blockIdx.x;
+  const int64_t col = strip * 128 + lc * 8;
+  const int64_t r0 = int64_t(blockIdx.y) * 128;
+  const bool col_ok = col < a.n;
+  const char* xb = a.x + b * a.sxb * EB;
+  Chunk<DT> raw[CPT];
+#pragma unroll
+  for (int p = 0; p < CPT; ++p) {
+    const int64_t r = r0 + p * 16 + rs;
+    if (r < a.m && col_ok) load_chunk<DT>(raw[p], xb + (r * a.sxm + col) * EB);
+    else zero_chunk<DT>(raw[p]);
+  }
+  float qs[8];
+  const uint32_t* amax_bits = reinterpret_cast<const uint32_t*>(a.scale) + b * a.ssb;
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+    qs[i] = col_ok ? channel_scales(__uint_as_float(amax_bits[(col + i) * a.ssn]), a.fp8_max, a.eps).qs : 0.0f;
+  uint8_t* yb = a.y + b * a.syb;
+#pragma unroll
+  for (int p = 0; p < CPT; ++p) {
+    const int64_t r = r0 + p * 16 + rs;
+    if (r < a.m && col_ok) {
+      float v[8];
+      unpack_chunk<DT>(raw[p], v);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) v[i] = clamp_sym(v[i] * qs[i], a.fp8_max);
+      store8<DT, NTS>(yb + r * a.sym + col,
+                      make_uint2(pack4<FMT>(v[0], v[1], v[2], v[3]), pack4<FMT>(v[4], v[5], v[6], v[7])));
+    }
+  }
+}
+
+// scale[b, c]: column maximum -> dequant scale max(amax, eps) / fp8_max
+__global__ __launch_bounds__(kThreads) void colchan_finalize_kernel(ColArgs a) {
+  const int64_t i = int64_t(blockIdx.x) * kThreads + threadIdx.x;
+  if (i >= (a.units / a.strips) * a.n) return;
+  const int64_t b = i / a.n, c = i - b * a.n;
+  float* s = a.scale + b * a.ssb + c * a.ssn;
+  *s = channel_scales(__uint_as_float(*reinterpret_cast<const uint32_t*>(s)), a.fp8_max, a.eps).ds;
+}
+
+// ===========================================================================
 // dual block quantization: 1 x 128 groups along n and 128 x 1 groups along m
 // of one row-contiguous tensor from a single read
 // ===========================================================================
@@ -919,6 +1033,24 @@ struct LaunchDual {
 };
 
 template <int DT, int FMT>
+struct LaunchColChan {
+  template <bool NTS>
+  static int go(const ColArgs& a, int64_t batch, hipStream_t st) {
+    const int lin = static_cast<int>((batch * a.n + kThreads - 1) / kThreads);
+    const dim3 grid(static_cast<uint32_t>(a.strips), static_cast<uint32_t>((a.m + 127) / 128),
+                    static_cast<uint32_t>(batch));
+    colchan_zero_kernel<<<lin, kThreads, 0, st>>>(a);
+    colchan_amax_kernel<DT><<<grid, kThreads, 0, st>>>(a);
+    colchan_apply_kernel<DT, FMT, NTS><<<grid, kThreads, 0, st>>>(a);
+    colchan_finalize_kernel<<<lin, kThreads, 0, st>>>(a);
+    return check_launch("per-column kernels");
+  }
+  static int run(const ColArgs& a, int64_t batch, hipStream_t st) {
+    return nt_stores() ? go<true>(a, batch, st) : go<false>(a, batch, st);
+  }
+};
+
+template <int DT, int FMT>
 struct LaunchCols {
   static int run(const ColArgs& a, bool channel, hipStream_t st) {
     const int grid = grid_for(a.units);
@@ -1151,6 +1283,12 @@ extern "C" int pcamd_quant_channel(const void* x, int x_dtype, int64_t batch, in
     a.strips = (n + 127) / 128; a.groups = 1; a.units = batch * a.strips;
     a.group_rows = static_cast<int32_t>(std::min<int64_t>(m, INT32_MAX)); a.rpt = 0;
     a.fp8_max = fp8_max; a.eps = eps;
+    // Tall tensors: 128-row slabs in parallel (column maxima by atomic max in
+    // the scale slots, then a quantize pass). Up to 256 rows one workgroup
+    // per strip reads its rows twice.
+    if (m > 256 && a.strips <= INT32_MAX && (m + 127) / 128 <= 65535 && batch <= 65535 &&
+        (batch * n + kThreads - 1) / kThreads <= INT32_MAX)
+      return dispatch_dt_fmt<LaunchColChan>(x_dtype, y_dtype, a, batch, st);
     return dispatch_dt_fmt<LaunchCols>(x_dtype, y_dtype, a, true, st);
   }
   GenArgs a{};

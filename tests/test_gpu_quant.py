@@ -305,9 +305,11 @@ CHANNEL_CASES = [
     ((2, 40, 7168), "bf16", -2, "e4m3"),    # 14 chunk slots per lane
     ((2, 16, 8200), "bf16", -2, "e4m3"),    # longer than 8192: generic two-pass row
     ((50, 70), "f32", -2, "e4m3"),          # generic (n % 8 != 0)
-    ((3, 300, 264), "bf16", -1, "e4m3"),    # column strips
+    ((3, 300, 264), "bf16", -1, "e4m3"),    # row slabs + atomic column maxima, ragged strip
+    ((200, 264), "bf16", -1, "e4m3"),       # column strips (<= 256 rows)
     ((50, 70), "f32", -1, "e5m2"),          # generic columns
-    ((1, 4096, 512), "f16", -1, "e4m3"),    # tall column strips
+    ((1, 4096, 512), "f16", -1, "e4m3"),    # row slabs
+    ((1000, 136), "f32", -1, "e5m2"),       # row slabs, ragged last slab, fp32
     ((64, 1024), "f32", -2, "e5m2"),        # fp32 rows
 ]
 
@@ -329,6 +331,20 @@ def test_channel_one_pass_same_bytes(dev):
     assert a.meta["quant_strategy"] == "one_pass" and b.meta["quant_strategy"] == "two_pass"
     assert torch.equal(a.tensor.view(torch.uint8), b.tensor.view(torch.uint8))
     assert torch.equal(a.dequant_scale, b.dequant_scale)
+
+
+def test_columns_full_size(dev):
+    """One scale per column (channel_axis=-1, the reference bench's default
+    axis and the per-channel BMM's B operand) over the config-2 weight
+    [18432, 7168]: 144 row slabs meet in each column's atomic maximum."""
+    g = torch.Generator().manual_seed(3)
+    w = (torch.randn(18432, 7168, generator=g) * 0.02)
+    w[12345, 77] = 9.0                       # a lone column maximum deep in the tensor
+    w = w.bfloat16()
+    r = hip_per_channel_quant(w.to(dev), channel_axis=-1)
+    q_ref, s_ref = O.quant_channel(w, -1, threads=8)
+    assert r.dequant_scale.shape == (7168,)
+    assert_same(r, q_ref, s_ref, "columns full size")
 
 
 def test_config2_full_size(dev):
