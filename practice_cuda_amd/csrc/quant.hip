@@ -32,7 +32,8 @@
 //   quant_*_generic     any strides / block shape; one workgroup per block or
 //                       channel, two passes (second read served by L2).
 //   per-tensor          amax kernel (workgroup max + one atomic max on the
-//                       fp32 bit pattern), quantize kernel, finalize kernel.
+//                       fp32 bit pattern), quantize kernel, finalize kernel;
+//                       contiguous tensors as one run of 16-byte chunks.
 //
 // Reference semantics (xuOAO/practice_cuda):
 //   kernels/quant/per_block.py:35-48, kernels/quant/per_channel.py:136-267,
@@ -531,6 +532,68 @@ __global__ __launch_bounds__(kThreads) void tensor_quant_kernel(TensorArgs a) {
     const int64_t r = rem / a.n, c = rem - r * a.n;
     const float v = load_one<DT>(a.x, b * a.sxb + r * a.sxm + c * a.sxn);
     a.y[b * a.syb + r * a.sym + c * a.syn] = static_cast<uint8_t>(quant_one<DT, FMT>(v, s.qs, a.fp8_max));
+  }
+}
+
+// Contiguous input and output (total % 8 == 0, 16-byte aligned): the tensor
+// as one run of 8-element chunks. amax: at most 256 workgroups of 512 threads
+// striding over units of 8 chunks per lane, one atomic max per workgroup (one
+// atomic per workgroup on the single slot is the limit: 1792 non-persistent
+// workgroups finishing together took 27 us at [4096, 7168] against 13 us
+// here, and a device-scope read before the atomic does not help when they all
+// read an empty slot). quantize: units of two chunks per lane (the flat 1 x G
+// layout).
+constexpr int kAmaxThreads = 512;
+constexpr int kAmaxGrid = 256;
+
+template <int DT>
+__global__ __launch_bounds__(kAmaxThreads) void tensor_amax_flat_kernel(TensorArgs a) {
+  constexpr int EB = elem_bytes<DT>(), CPT = 8, W = kAmaxThreads / 64;
+  __shared__ float red[W];
+  const int64_t chunks = a.total / 8;
+  constexpr int64_t kUnit = int64_t(kAmaxThreads) * CPT;
+  float amax = 0.0f;
+  for (int64_t base = int64_t(blockIdx.x) * kUnit; base < chunks; base += int64_t(gridDim.x) * kUnit) {
+    Chunk<DT> c[CPT];
+#pragma unroll
+    for (int p = 0; p < CPT; ++p) {
+      const int64_t ch = base + p * kAmaxThreads + threadIdx.x;
+      if (ch < chunks) load_chunk<DT>(c[p], a.x + ch * 8 * EB);
+      else zero_chunk<DT>(c[p]);
+    }
+#pragma unroll
+    for (int p = 0; p < CPT; ++p) amax = fmaxf(amax, chunk_amax<DT>(c[p]));
+  }
+  amax = group_max<64>(amax);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = amax;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+#pragma unroll
+    for (int w = 1; w < W; ++w) amax = fmaxf(amax, red[w]);
+    atomicMax(reinterpret_cast<uint32_t*>(a.scale), __float_as_uint(amax));
+  }
+}
+
+template <int DT, int FMT, bool NTS>
+__global__ __launch_bounds__(kGroupThreads) void tensor_quant_flat_kernel(TensorArgs a) {
+  constexpr int EB = elem_bytes<DT>(), CPL = 2;
+  const int64_t chunks = a.total / 8;
+  const int lane = threadIdx.x & 63;
+  const int64_t u = int64_t(blockIdx.x) * (kGroupThreads / 64) + (threadIdx.x >> 6);
+  const int64_t ch0 = u * (CPL * 64) + lane;
+  Chunk<DT> cur[CPL];
+#pragma unroll
+  for (int c = 0; c < CPL; ++c) {
+    const int64_t ch = ch0 + c * 64;
+    if (ch < chunks) load_chunk<DT>(cur[c], a.x + ch * 8 * EB);
+    else zero_chunk<DT>(cur[c]);
+  }
+  const Scales s = tensor_scales(__uint_as_float(*reinterpret_cast<const uint32_t*>(a.scale)), a.fp8_max, a.eps,
+                                 a.scale_dt);
+#pragma unroll
+  for (int c = 0; c < CPL; ++c) {
+    const int64_t ch = ch0 + c * 64;
+    if (ch < chunks) store8<DT, NTS>(a.y + ch * 8, quant_chunk<DT, FMT>(cur[c], s.qs, a.fp8_max));
   }
 }
 
@@ -1073,11 +1136,20 @@ struct LaunchGeneric {
 
 template <int DT, int FMT>
 struct LaunchTensor {
-  static int run(const TensorArgs& a, hipStream_t st) {
+  static int run(const TensorArgs& a, bool flat, hipStream_t st) {
     fill_zero_u32_kernel<<<1, 1, 0, st>>>(reinterpret_cast<uint32_t*>(a.scale));
-    const int grid = grid_for(a.total, kThreads, 4096);
-    if (a.total > 0) tensor_amax_kernel<DT><<<grid, kThreads, 0, st>>>(a);
-    if (a.total > 0) tensor_quant_kernel<DT, FMT><<<grid, kThreads, 0, st>>>(a);
+    if (a.total > 0 && flat) {
+      const int64_t chunks = a.total / 8;
+      tensor_amax_flat_kernel<DT><<<grid_for(chunks, kAmaxThreads * 8, kAmaxGrid), kAmaxThreads, 0, st>>>(a);
+      const int64_t waves = (chunks + 127) / 128;
+      const int grid = static_cast<int>((waves + kGroupThreads / 64 - 1) / (kGroupThreads / 64));
+      if (nt_stores()) tensor_quant_flat_kernel<DT, FMT, true><<<grid, kGroupThreads, 0, st>>>(a);
+      else tensor_quant_flat_kernel<DT, FMT, false><<<grid, kGroupThreads, 0, st>>>(a);
+    } else if (a.total > 0) {
+      const int grid = grid_for(a.total, kThreads, 4096);
+      tensor_amax_kernel<DT><<<grid, kThreads, 0, st>>>(a);
+      tensor_quant_kernel<DT, FMT><<<grid, kThreads, 0, st>>>(a);
+    }
     tensor_finalize_kernel<<<1, 1, 0, st>>>(a);
     return check_launch("per-tensor kernels");
   }
@@ -1318,7 +1390,10 @@ extern "C" int pcamd_quant_tensor(const void* x, int x_dtype, int64_t batch, int
   a.batch = batch; a.m = m; a.n = n; a.sxb = sxb; a.sxm = sxm; a.sxn = sxn;
   a.syb = syb; a.sym = sym; a.syn = syn; a.total = batch * m * n;
   a.fp8_max = fp8_max; a.eps = eps; a.scale_dt = scale_dtype;
-  return dispatch_dt_fmt<LaunchTensor>(x_dtype, y_dtype, a, static_cast<hipStream_t>(stream));
+  // one contiguous run of whole chunks in and out
+  const bool flat = row_fast_ok(x, x_dtype, y, n, sxb, sxm, sxn, syb, sym, syn) && sxm == n && sym == n &&
+                    (batch == 1 || (sxb == m * n && syb == m * n)) && (a.total / 8 + 127) / 128 < (1LL << 31);
+  return dispatch_dt_fmt<LaunchTensor>(x_dtype, y_dtype, a, flat, static_cast<hipStream_t>(stream));
 }
 
 extern "C" int pcamd_selftest_fp8_convert(int fmt, uint32_t* result, void* stream) {
