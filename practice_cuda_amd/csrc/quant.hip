@@ -844,17 +844,17 @@ struct DualArgs {
   float fp8_max, eps;
 };
 
-// Grid (128-column strips, 128-row groups, batch), 256 threads. Lane t holds
-// columns 8 (t % 16) .. + 7 of rows t / 16 + 16 p (p < 8) of the 128 x 128
-// block, loaded up front. Each row's 128 columns sit in one aligned 16-lane
+// Grid (128-column strips, 128-row groups, batch), NT threads. Lane t holds
+// columns 8 (t % 16) .. + 7 of rows t / 16 + (NT / 16) p (p < 2048 / NT) of
+// the 128 x 128 block, loaded up front. Each row's 128 columns sit in one aligned 16-lane
 // row of the wave (DPP max); column maxima meet as in quant_colgroup_kernel
 // (lane shuffles, then LDS across the waves). The results are those of the
 // 1 x 128 and 128 x 1 quantizers run separately. FULL: m and n are multiples
 // of 128, so no bounds checks.
-template <int DT, int FMT, bool NTS, bool FULL>
-__global__ __launch_bounds__(kThreads) void quant_dual_kernel(DualArgs a) {
+template <int DT, int FMT, int NT, bool NTS, bool FULL>
+__global__ __launch_bounds__(NT) void quant_dual_kernel(DualArgs a) {
   constexpr int EB = elem_bytes<DT>();
-  constexpr int CPT = 8, WAVES = kThreads / 64;
+  constexpr int CPT = 2048 / NT, WAVES = NT / 64, RPP = NT / 16;
   __shared__ float part[WAVES][128];
   __shared__ float qsv[128];
   const int t = threadIdx.x;
@@ -866,7 +866,7 @@ __global__ __launch_bounds__(kThreads) void quant_dual_kernel(DualArgs a) {
   Chunk<DT> raw[CPT];
 #pragma unroll
   for (int p = 0; p < CPT; ++p) {
-    const int64_t r = r0 + p * 16 + rs;
+    const int64_t r = r0 + p * RPP + rs;
     if (FULL || (r < a.m && col < a.n)) load_chunk<DT>(raw[p], xb + (r * a.sxm + col) * EB);
     else zero_chunk<DT>(raw[p]);
   }
@@ -876,7 +876,7 @@ __global__ __launch_bounds__(kThreads) void quant_dual_kernel(DualArgs a) {
   for (int p = 0; p < CPT; ++p) {
     const Scales s = block_scales(group_max<16>(chunk_amax<DT>(raw[p])), a.fp8_max, a.eps);
     rq[p] = s.qs;
-    const int64_t r = r0 + p * 16 + rs;
+    const int64_t r = r0 + p * RPP + rs;
     if (lc == 0 && (FULL || r < a.m)) a.sr[b * a.srb + r * a.srm + strip * a.srn] = s.ds;
   }
   // 128 x 1: one group per column of the strip
@@ -915,7 +915,7 @@ __global__ __launch_bounds__(kThreads) void quant_dual_kernel(DualArgs a) {
   uint8_t* ycb = a.yc + b * a.syb;
 #pragma unroll
   for (int p = 0; p < CPT; ++p) {
-    const int64_t r = r0 + p * 16 + rs;
+    const int64_t r = r0 + p * RPP + rs;
     if (FULL || (r < a.m && col < a.n)) {
       store8<DT, NTS>(yrb + r * a.sym + col, quant_chunk<DT, FMT>(raw[p], rq[p], a.fp8_max));
       float v[8];
@@ -1086,8 +1086,9 @@ struct LaunchDual {
   static int go(const DualArgs& a, int64_t batch, hipStream_t st) {
     const dim3 grid(static_cast<uint32_t>((a.n + 127) / 128), static_cast<uint32_t>((a.m + 127) / 128),
                     static_cast<uint32_t>(batch));
-    if (a.m % 128 == 0 && a.n % 128 == 0) quant_dual_kernel<DT, FMT, NTS, true><<<grid, kThreads, 0, st>>>(a);
-    else quant_dual_kernel<DT, FMT, NTS, false><<<grid, kThreads, 0, st>>>(a);
+    constexpr int NT = 512;  // 256: 3 % slower at [8192, 14336]; 1024: 4 % slower
+    if (a.m % 128 == 0 && a.n % 128 == 0) quant_dual_kernel<DT, FMT, NT, NTS, true><<<grid, NT, 0, st>>>(a);
+    else quant_dual_kernel<DT, FMT, NT, NTS, false><<<grid, NT, 0, st>>>(a);
     return check_launch("quant_dual_kernel");
   }
   static int run(const DualArgs& a, int64_t batch, hipStream_t st) {
