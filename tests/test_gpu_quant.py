@@ -347,6 +347,19 @@ def test_columns_full_size(dev):
     assert_same(r, q_ref, s_ref, "columns full size")
 
 
+def test_columns_microbench_shape(dev):
+    """The reference's per-channel microbench point
+    (fp8_training/microbench/profile_fused_quant.py:27-35): fp32 [80, 2048,
+    1280], channel_axis=-1, eps 1e-6; seeded on the CPU (the reference draws
+    on the device)."""
+    g = torch.Generator().manual_seed(4)
+    x = torch.randn(80, 2048, 1280, generator=g)
+    r = hip_per_channel_quant(x.to(dev), channel_axis=-1, eps=1e-6)
+    q_ref, s_ref = O.quant_channel(x, -1, eps=1e-6, threads=8)
+    assert r.dequant_scale.shape == (80, 1280)
+    assert_same(r, q_ref, s_ref, "microbench per-column")
+
+
 def test_config2_full_size(dev):
     """bf16 weight [18432, 7168] N(0, 0.02), one scale per row."""
     g = torch.Generator().manual_seed(0)
