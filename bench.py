@@ -369,18 +369,57 @@ def cpu_baseline(torch, x_cpu):
             "sample": f"bf16 [{m},{n}] (the full workload tensor), "
                       f"median of 5 runs of oracle/fp8_oracle.c per-channel quant, "
                       f"{threads} OpenMP threads, {t * 1e3:.1f} ms/run",
-            "torch_eager": torch_eager_baseline(torch, sample, threads)}
+            "torch_eager": torch_eager_baseline(torch, sample, threads),
+            "config0": config0_baseline(torch, threads)}
 
 
 def torch_channel_quant(torch, x, fp8_max=448.0, eps=1e-12):
     """The reference's PyTorch form of the per-row quantizer
     (kernels/quant/per_channel.py:9-29, channel_axis=-2): fp32 math, amax
     per row, s = max(amax, eps), q = fp8(clamp(x * (fp8_max / s))), scale
-    s / fp8_max."""
+    s / fp8_max. fp8_max / s is a true fp32 division, as in the reference's
+    Triton kernels and its compiled form; eager `float / tensor` would
+    compute reciprocal(s) * fp8_max, which differs in the last bit for some
+    s."""
     xf = x.float()
     s = xf.abs().amax(dim=-1, keepdim=True).clamp(min=eps)
-    q = (xf * (fp8_max / s)).clamp(-fp8_max, fp8_max).to(torch.float8_e4m3fn)
+    qs = torch.full_like(s, fp8_max) / s  # a true division (scalar / tensor is reciprocal * scalar)
+    q = (xf * qs).clamp(-fp8_max, fp8_max).to(torch.float8_e4m3fn)
     return q, (s / fp8_max).squeeze(-1)
+
+
+def torch_group_quant(torch, x, group=128, fp8_max=448.0, eps=1e-12):
+    """The reference's 1 x 128 group quantizer in eager PyTorch (the math of
+    kernels/quant/per_block.py:35-48): per group s = max(amax, eps),
+    qs = fp8_max / s, q = fp8(clamp(x * qs)), scale 1 / qs."""
+    m, n = x.shape
+    xf = x.float().view(m, n // group, group)
+    s = xf.abs().amax(dim=-1, keepdim=True).clamp(min=eps)
+    qs = torch.full_like(s, fp8_max) / s  # a true division (scalar / tensor is reciprocal * scalar)
+    q = (xf * qs).clamp(-fp8_max, fp8_max).to(torch.float8_e4m3fn).view(m, n)
+    return q, (1.0 / qs).squeeze(-1)
+
+
+def config0_baseline(torch, threads):
+    """the 1 x 128 quantizer of config 1's input through
+    eager PyTorch on the host cores, checked against the oracle."""
+    from oracle import oracle as O
+    x = make_config1(torch)
+    q_ref, s_ref = O.quant_block(x[:64], 1, 128, threads=threads)
+    torch.set_num_threads(threads)  # after the oracle call: both set the process's OpenMP thread count
+    q, s = torch_group_quant(torch, x[:64])
+    same = bool((q.view(torch.uint8).numpy() == q_ref).all() and (s.numpy().view("uint32") == s_ref.view("uint32")).all())
+    times = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        torch_group_quant(torch, x)
+        times.append(time.perf_counter() - t0)
+    t = statistics.median(times)
+    m, n = x.shape
+    nbytes = m * n * 3 + m * (n // 128) * 4
+    return {"value": nbytes / t / 1e9, "unit": "GB/s", "threads": torch.get_num_threads(), "matches_oracle": same,
+            "sample": f"BASELINE configs[0]: bf16 [{m},{n}] 1x128 groups, median of 3 runs of the eager-PyTorch "
+                      f"group quantizer (fp32 math), {t * 1e3:.1f} ms/run"}
 
 
 def torch_eager_baseline(torch, sample, threads):
