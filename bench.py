@@ -172,7 +172,7 @@ def quant_dual_launcher(torch, L, xs, yrs, ycs, srs, scs):
         yr, yc, sr, sc = yrs[i % len(yrs)], ycs[i % len(ycs)], srs[i % len(srs)], scs[i % len(scs)]
         rc = L.lib().pcamd_quant_block_dual(
             L.ptr(x), L.BF16, 1, x.shape[0], x.shape[1], 0, x.stride(0), 1,
-            L.ptr(yr), L.ptr(yc), L.E4M3FN, 0, yr.stride(0), 1,
+            L.ptr(yr), 0, yr.stride(0), 1, L.ptr(yc), 0, 1, x.shape[0], L.E4M3FN,
             L.ptr(sr), 0, sr.stride(0), 1, L.ptr(sc), 0, sc.stride(0), 1, 128, 448.0, 1e-12,
             L.stream_of(x))
         L.check(rc, "pcamd_quant_block_dual")
@@ -180,12 +180,13 @@ def quant_dual_launcher(torch, L, xs, yrs, ycs, srs, scs):
 
 
 def bench_quant_dual(torch, name, x_dev, steps, warmup, nsets, dev):
-    """1x128 and 128x1 quantization of one bf16 [m, n] tensor in one kernel."""
+    """1x128 and 128x1 quantization of one bf16 [m, n] tensor in one kernel, the
+    128x1 result stored transposed (as the training layer keeps it)."""
     from practice_cuda_amd import _lib as L
     m, n = x_dev.shape
     xs = [x_dev] + [x_dev.view(torch.int16).bitwise_xor(i & 1).view(torch.bfloat16) for i in range(1, nsets)]
     yrs = [torch.empty(m, n, dtype=torch.float8_e4m3fn, device=dev) for _ in range(nsets)]
-    ycs = [torch.empty(m, n, dtype=torch.float8_e4m3fn, device=dev) for _ in range(nsets)]
+    ycs = [torch.empty(n, m, dtype=torch.float8_e4m3fn, device=dev) for _ in range(nsets)]  # 128x1 stored transposed
     srs = [torch.empty(m, n // 128, dtype=torch.float32, device=dev) for _ in range(nsets)]
     scs = [torch.empty(m // 128, n, dtype=torch.float32, device=dev) for _ in range(nsets)]
     ms, samples = graph_time(torch, quant_dual_launcher(torch, L, xs, yrs, ycs, srs, scs), steps, warmup)

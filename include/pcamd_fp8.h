@@ -76,24 +76,28 @@ int pcamd_quant_block(const void *x, int x_dtype, int64_t batch, int64_t m,
  * Both block quantizations the block-scaled training recipe applies to one
  * tensor, from a single read of x: y_row / scale_row are exactly
  * pcamd_quant_block(block_m = 1, block_n = block) and y_col / scale_col
- * exactly pcamd_quant_block(block_m = block, block_n = 1). y_row and y_col
- * share the strides syb, sym, syn; scale_row is [batch, m, ceil(n / block)]
- * and scale_col [batch, ceil(m / block), n] (strides in elements). One kernel
- * serves row-contiguous x with block = 128; other layouts and block sizes run
- * the two quantizers in turn. The reference has no single counterpart: its
- * per-block training module is unfinished
+ * exactly pcamd_quant_block(block_m = block, block_n = 1). y_row has strides
+ * syb, sym, syn and y_col its own ycb, ycm, ycn: the same layout, or stored
+ * transposed (ycm = 1, element (r, c) at c * ycn + r), which makes it the
+ * K-major operand of a GEMM reducing over m. scale_row is
+ * [batch, m, ceil(n / block)] and scale_col [batch, ceil(m / block), n]
+ * (strides in elements). One kernel serves row-contiguous x with block = 128
+ * (transposed y_col: m and n multiples of 128, 16-byte aligned rows); other
+ * layouts and block sizes run the two quantizers in turn. The reference has no
+ * single counterpart: its per-block training module is unfinished
  * (fp8_training/fp8_bench/modules/per_block.py:13-67), and this pairs the
  * act/grad 1x128 quantization (impls/triton_per_block.py:60-150, block_m = 1)
  * with the wgrad re-quantization along the reduction dimension.
  */
 int pcamd_quant_block_dual(const void *x, int x_dtype, int64_t batch,
                            int64_t m, int64_t n, int64_t sxb, int64_t sxm,
-                           int64_t sxn, void *y_row, void *y_col, int y_dtype,
-                           int64_t syb, int64_t sym, int64_t syn,
-                           float *scale_row, int64_t srb, int64_t srm,
-                           int64_t srn, float *scale_col, int64_t scb,
-                           int64_t scm, int64_t scn, int64_t block,
-                           float fp8_max, float eps, void *stream);
+                           int64_t sxn, void *y_row, int64_t syb, int64_t sym,
+                           int64_t syn, void *y_col, int64_t ycb, int64_t ycm,
+                           int64_t ycn, int y_dtype, float *scale_row,
+                           int64_t srb, int64_t srm, int64_t srn,
+                           float *scale_col, int64_t scb, int64_t scm,
+                           int64_t scn, int64_t block, float fp8_max, float eps,
+                           void *stream);
 
 /*
  * Per-channel quantization. channel_axis = -2: one scale per row (reduce over

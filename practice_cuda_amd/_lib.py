@@ -60,7 +60,7 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.pcamd_quant_block.argtypes = quant_head + [_ptr, _i64, _i64, _i64, _i64, _i64, _flt, _flt, _ptr]
     lib.pcamd_quant_block_dual.restype = _int
     lib.pcamd_quant_block_dual.argtypes = (
-        [_ptr, _int, _i64, _i64, _i64, _i64, _i64, _i64, _ptr, _ptr, _int, _i64, _i64, _i64]
+        [_ptr, _int, _i64, _i64, _i64, _i64, _i64, _i64] + [_ptr, _i64, _i64, _i64] * 2 + [_int]
         + [_ptr, _i64, _i64, _i64] * 2 + [_i64, _flt, _flt, _ptr])
     lib.pcamd_quant_channel.restype = _int
     lib.pcamd_quant_channel.argtypes = quant_head + [_ptr, _i64, _i64, _int, _flt, _flt, _ptr]

@@ -835,28 +835,50 @@ __global__ __launch_bounds__(kThreads) void colchan_finalize_kernel(ColArgs a) {
 struct DualArgs {
   const char* x;
   uint8_t* yr;            // fp8 output of the 1 x 128 groups
-  uint8_t* yc;            // fp8 output of the 128 x 1 groups (same strides as yr)
+  uint8_t* yc;            // fp8 output of the 128 x 1 groups
   float* sr;              // row-group scales [b, row, strip]
   float* sc;              // column-group scales [b, row group, col]
   int64_t m, n;
   int64_t sxb, sxm, syb, sym;
+  int64_t ycb, ycn;       // yc strides (bytes) when it is stored transposed (element (r, c) at c * ycn + r)
   int64_t srb, srm, srn, scb, scm, scn;
   float fp8_max, eps;
 };
 
+// 4 x 4 byte transpose: byte j of d[i] -> byte i of e[j]
+PCAMD_DEV void byte_transpose4(uint32_t d0, uint32_t d1, uint32_t d2, uint32_t d3, uint32_t (&e)[4]) {
+  const uint32_t lo01 = __builtin_amdgcn_perm(d1, d0, 0x05010400u);  // d0.b0 d1.b0 d0.b1 d1.b1
+  const uint32_t hi01 = __builtin_amdgcn_perm(d1, d0, 0x07030602u);  // d0.b2 d1.b2 d0.b3 d1.b3
+  const uint32_t lo23 = __builtin_amdgcn_perm(d3, d2, 0x05010400u);
+  const uint32_t hi23 = __builtin_amdgcn_perm(d3, d2, 0x07030602u);
+  e[0] = __builtin_amdgcn_perm(lo23, lo01, 0x05040100u);
+  e[1] = __builtin_amdgcn_perm(lo23, lo01, 0x07060302u);
+  e[2] = __builtin_amdgcn_perm(hi23, hi01, 0x05040100u);
+  e[3] = __builtin_amdgcn_perm(hi23, hi01, 0x07060302u);
+}
+
 // Grid (128-column strips, 128-row groups, batch), NT threads. Lane t holds
 // columns 8 (t % 16) .. + 7 of rows t / 16 + (NT / 16) p (p < 2048 / NT) of
-// the 128 x 128 block, loaded up front. Each row's 128 columns sit in one aligned 16-lane
+// the 128 x 128 block, loaded up front (TCOL: rows 4 (t / 16) + p, p < 4).
+// TCOL: the 128 x 1 output is stored transposed (element (r, c) at
+// c * ycn + r): each lane turns its 4 rows x 8 columns of fp8 bytes into 8
+// words of 4 rows (byte transposes), the block passes through 16 KiB of LDS,
+// and the transposed rows leave as 16-byte stores. Needs whole blocks. Each row's 128 columns sit in one aligned 16-lane
 // row of the wave (DPP max); column maxima meet as in quant_colgroup_kernel
 // (lane shuffles, then LDS across the waves). The results are those of the
 // 1 x 128 and 128 x 1 quantizers run separately. FULL: m and n are multiples
 // of 128, so no bounds checks.
-template <int DT, int FMT, int NT, bool NTS, bool FULL>
+template <int DT, int FMT, int NT, bool NTS, bool FULL, bool TCOL>
 __global__ __launch_bounds__(NT) void quant_dual_kernel(DualArgs a) {
   constexpr int EB = elem_bytes<DT>();
   constexpr int CPT = 2048 / NT, WAVES = NT / 64, RPP = NT / 16;
+  static_assert(!TCOL || (FULL && CPT == 4), "transposed column output: whole blocks, four rows per lane");
   __shared__ float part[WAVES][128];
   __shared__ float qsv[128];
+  // transposed block: 128 columns x 32 words of 4 rows; the 16-byte groups of
+  // column c sit XOR-ed with (c / 8) % 8 so that the word writes are at most
+  // 2-way bank conflicted and the reads are whole 16-byte groups
+  __shared__ __attribute__((aligned(16))) uint32_t tt[TCOL ? 128 * 32 : 1];
   const int t = threadIdx.x;
   const int lc = t & 15, rs = t >> 4;
   const int64_t b = blockIdx.z, g = blockIdx.y, strip = blockIdx.x;
@@ -866,7 +888,7 @@ __global__ __launch_bounds__(NT) void quant_dual_kernel(DualArgs a) {
   Chunk<DT> raw[CPT];
 #pragma unroll
   for (int p = 0; p < CPT; ++p) {
-    const int64_t r = r0 + p * RPP + rs;
+    const int64_t r = TCOL ? r0 + 4 * rs + p : r0 + p * RPP + rs;
     if (FULL || (r < a.m && col < a.n)) load_chunk<DT>(raw[p], xb + (r * a.sxm + col) * EB);
     else zero_chunk<DT>(raw[p]);
   }
@@ -876,7 +898,7 @@ __global__ __launch_bounds__(NT) void quant_dual_kernel(DualArgs a) {
   for (int p = 0; p < CPT; ++p) {
     const Scales s = block_scales(group_max<16>(chunk_amax<DT>(raw[p])), a.fp8_max, a.eps);
     rq[p] = s.qs;
-    const int64_t r = r0 + p * RPP + rs;
+    const int64_t r = TCOL ? r0 + 4 * rs + p : r0 + p * RPP + rs;
     if (lc == 0 && (FULL || r < a.m)) a.sr[b * a.srb + r * a.srm + strip * a.srn] = s.ds;
   }
   // 128 x 1: one group per column of the strip
@@ -912,18 +934,40 @@ __global__ __launch_bounds__(NT) void quant_dual_kernel(DualArgs a) {
 #pragma unroll
   for (int i = 0; i < 8; ++i) qc[i] = qsv[lc * 8 + i];
   uint8_t* yrb = a.yr + b * a.syb;
-  uint8_t* ycb = a.yc + b * a.syb;
+  uint2 qcol[CPT];
 #pragma unroll
   for (int p = 0; p < CPT; ++p) {
-    const int64_t r = r0 + p * RPP + rs;
+    const int64_t r = TCOL ? r0 + 4 * rs + p : r0 + p * RPP + rs;
     if (FULL || (r < a.m && col < a.n)) {
       store8<DT, NTS>(yrb + r * a.sym + col, quant_chunk<DT, FMT>(raw[p], rq[p], a.fp8_max));
       float v[8];
       unpack_chunk<DT>(raw[p], v);
 #pragma unroll
       for (int i = 0; i < 8; ++i) v[i] = clamp_sym(v[i] * qc[i], a.fp8_max);
-      store8<DT, NTS>(ycb + r * a.sym + col,
-                      make_uint2(pack4<FMT>(v[0], v[1], v[2], v[3]), pack4<FMT>(v[4], v[5], v[6], v[7])));
+      qcol[p] = make_uint2(pack4<FMT>(v[0], v[1], v[2], v[3]), pack4<FMT>(v[4], v[5], v[6], v[7]));
+      if constexpr (!TCOL) store8<DT, NTS>(a.yc + b * a.syb + r * a.sym + col, qcol[p]);
+    }
+  }
+  if constexpr (TCOL) {
+    // word w[i] of this lane: rows 4 rs .. 4 rs + 3 of column lc * 8 + i
+    uint32_t w[8];
+    byte_transpose4(qcol[0].x, qcol[1].x, qcol[2].x, qcol[3].x, reinterpret_cast<uint32_t(&)[4]>(w[0]));
+    byte_transpose4(qcol[0].y, qcol[1].y, qcol[2].y, qcol[3].y, reinterpret_cast<uint32_t(&)[4]>(w[4]));
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int c = lc * 8 + i;
+      tt[c * 32 + (((rs >> 2) ^ (lc & 7)) << 2) + (rs & 3)] = w[i];
+    }
+    __syncthreads();
+    uint8_t* ycb = a.yc + b * a.ycb + (strip * 128) * a.ycn + r0;
+#pragma unroll
+    for (int j = 0; j < 1024 / NT; ++j) {
+      const int q = t + j * NT;           // 16-byte piece: column q / 8, rows 16 (q % 8) .. + 15
+      const int ct = q >> 3, seg = q & 7;
+      const u32x4_t v = *reinterpret_cast<const u32x4_t*>(tt + ct * 32 + ((seg ^ ((ct >> 3) & 7)) << 2));
+      uint8_t* dst = ycb + ct * a.ycn + seg * 16;
+      if constexpr (NTS) __builtin_nontemporal_store(v, reinterpret_cast<u32x4_t*>(dst));
+      else *reinterpret_cast<u32x4_t*>(dst) = v;
     }
   }
 }
@@ -1083,16 +1127,18 @@ struct LaunchColGroups {
 template <int DT, int FMT>
 struct LaunchDual {
   template <bool NTS>
-  static int go(const DualArgs& a, int64_t batch, hipStream_t st) {
+  static int go(const DualArgs& a, int64_t batch, bool tcol, hipStream_t st) {
     const dim3 grid(static_cast<uint32_t>((a.n + 127) / 128), static_cast<uint32_t>((a.m + 127) / 128),
                     static_cast<uint32_t>(batch));
     constexpr int NT = 512;  // 256: 3 % slower at [8192, 14336]; 1024: 4 % slower
-    if (a.m % 128 == 0 && a.n % 128 == 0) quant_dual_kernel<DT, FMT, NT, NTS, true><<<grid, NT, 0, st>>>(a);
-    else quant_dual_kernel<DT, FMT, NT, NTS, false><<<grid, NT, 0, st>>>(a);
+    const bool full = a.m % 128 == 0 && a.n % 128 == 0;
+    if (tcol) quant_dual_kernel<DT, FMT, NT, NTS, true, true><<<grid, NT, 0, st>>>(a);
+    else if (full) quant_dual_kernel<DT, FMT, NT, NTS, true, false><<<grid, NT, 0, st>>>(a);
+    else quant_dual_kernel<DT, FMT, NT, NTS, false, false><<<grid, NT, 0, st>>>(a);
     return check_launch("quant_dual_kernel");
   }
-  static int run(const DualArgs& a, int64_t batch, hipStream_t st) {
-    return nt_stores() ? go<true>(a, batch, st) : go<false>(a, batch, st);
+  static int run(const DualArgs& a, int64_t batch, bool tcol, hipStream_t st) {
+    return nt_stores() ? go<true>(a, batch, tcol, st) : go<false>(a, batch, tcol, st);
   }
 };
 
@@ -1272,10 +1318,10 @@ extern "C" int pcamd_quant_block(const void* x, int x_dtype, int64_t batch, int6
 }
 
 extern "C" int pcamd_quant_block_dual(const void* x, int x_dtype, int64_t batch, int64_t m, int64_t n,
-                                      int64_t sxb, int64_t sxm, int64_t sxn, void* y_row, void* y_col,
-                                      int y_dtype, int64_t syb, int64_t sym, int64_t syn,
-                                      float* scale_row, int64_t srb, int64_t srm, int64_t srn,
-                                      float* scale_col, int64_t scb, int64_t scm, int64_t scn,
+                                      int64_t sxb, int64_t sxm, int64_t sxn, void* y_row, int64_t syb,
+                                      int64_t sym, int64_t syn, void* y_col, int64_t ycb, int64_t ycm,
+                                      int64_t ycn, int y_dtype, float* scale_row, int64_t srb, int64_t srm,
+                                      int64_t srn, float* scale_col, int64_t scb, int64_t scm, int64_t scn,
                                       int64_t block, float fp8_max, float eps, void* stream) {
   clear_error();
   int rc = validate_common(x, x_dtype, batch, m, n, y_row, y_dtype, scale_row, fp8_max);
@@ -1287,22 +1333,27 @@ extern "C" int pcamd_quant_block_dual(const void* x, int x_dtype, int64_t batch,
     return set_error(PCAMD_ERR_INVALID, "block size must be a power of two, got %lld", (long long)block);
   if (batch == 0 || m == 0 || n == 0) return PCAMD_OK;
   hipStream_t st = static_cast<hipStream_t>(stream);
-  const bool fast = row_fast_ok(x, x_dtype, y_row, n, sxb, sxm, sxn, syb, sym, syn) && aligned(y_col, 8);
-  if (fast && block == 128 && batch <= 65535 && (m + 127) / 128 <= 65535 && (n + 127) / 128 <= INT32_MAX) {
+  const bool fast = row_fast_ok(x, x_dtype, y_row, n, sxb, sxm, sxn, syb, sym, syn) && block == 128 &&
+                    batch <= 65535 && (m + 127) / 128 <= 65535 && (n + 127) / 128 <= INT32_MAX;
+  const bool same_layout = ycb == syb && ycm == sym && ycn == syn && aligned(y_col, 8);
+  // transposed 128 x 1 output (element (r, c) at c * ycn + r): whole blocks, 16-byte aligned rows
+  const bool transposed = ycm == 1 && ycn >= m && m % 128 == 0 && n % 128 == 0 && ycn % 16 == 0 &&
+                          ycb % 16 == 0 && aligned(y_col, 16);
+  if (fast && (same_layout || transposed)) {
     DualArgs a{};
     a.x = static_cast<const char*>(x);
     a.yr = static_cast<uint8_t*>(y_row); a.yc = static_cast<uint8_t*>(y_col);
     a.sr = scale_row; a.sc = scale_col;
-    a.m = m; a.n = n; a.sxb = sxb; a.sxm = sxm; a.syb = syb; a.sym = sym;
+    a.m = m; a.n = n; a.sxb = sxb; a.sxm = sxm; a.syb = syb; a.sym = sym; a.ycb = ycb; a.ycn = ycn;
     a.srb = srb; a.srm = srm; a.srn = srn; a.scb = scb; a.scm = scm; a.scn = scn;
     a.fp8_max = fp8_max; a.eps = eps;
-    return dispatch_dt_fmt<LaunchDual>(x_dtype, y_dtype, a, batch, st);
+    return dispatch_dt_fmt<LaunchDual>(x_dtype, y_dtype, a, batch, !same_layout, st);
   }
   // other layouts and block sizes: the two quantizers one after the other
   rc = pcamd_quant_block(x, x_dtype, batch, m, n, sxb, sxm, sxn, y_row, y_dtype, syb, sym, syn, scale_row,
                          srb, srm, srn, 1, block, fp8_max, eps, stream);
   if (rc) return rc;
-  return pcamd_quant_block(x, x_dtype, batch, m, n, sxb, sxm, sxn, y_col, y_dtype, syb, sym, syn, scale_col,
+  return pcamd_quant_block(x, x_dtype, batch, m, n, sxb, sxm, sxn, y_col, y_dtype, ycb, ycm, ycn, scale_col,
                            scb, scm, scn, block, 1, fp8_max, eps, stream);
 }
 

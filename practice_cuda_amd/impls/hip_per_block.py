@@ -81,6 +81,7 @@ def hip_per_block_quant_dual(
     block: int = 128,
     fp8_dtype: torch.dtype = torch.float8_e4m3fn,
     eps: float = 1e-12,
+    col_transposed: bool = False,
 ) -> tuple[QuantResult, QuantResult]:
     """``(hip_per_block_quant(x, block_m=1, block_n=block), hip_per_block_quant(x,
     block_m=block, block_n=1))`` from one read of x.
@@ -89,6 +90,9 @@ def hip_per_block_quant_dual(
     activations and of the output gradient: 1 x block groups along the last
     dim for the forward / dgrad GEMMs, block x 1 groups along the rows for
     wgrad. The results are bit-identical to the two separate calls.
+    col_transposed: the block x 1 result is stored transposed (a [.., N, M]
+    contiguous buffer seen as [.., M, N]), so a GEMM that reduces over M reads
+    it K-major.
     """
     if x.ndim not in (2, 3):
         raise ValueError(f"per-block quant expects a 2D or 3D tensor, got {tuple(x.shape)}")
@@ -98,10 +102,13 @@ def hip_per_block_quant_dual(
     _lib.require_gpu_tensor(x, "x")
 
     out_row = torch.empty_like(x, dtype=fp8_dtype, memory_format=torch.preserve_format)
-    out_col = torch.empty_like(out_row)
-    batch, m, n, xs, ys = C.dims3(x, out_row)
-    if tuple(out_col.stride()) != tuple(out_row.stride()):
+    if col_transposed:
+        out_col = torch.empty(*x.shape[:-2], x.shape[-1], x.shape[-2], dtype=fp8_dtype,
+                              device=x.device).transpose(-1, -2)
+    else:
         out_col = torch.empty_strided(out_row.shape, out_row.stride(), dtype=fp8_dtype, device=x.device)
+    batch, m, n, xs, ys = C.dims3(x, out_row)
+    yc = (0, *out_col.stride()) if out_col.ndim == 2 else tuple(out_col.stride())
     s_row = torch.empty((batch, m, -(-n // block)), device=x.device, dtype=torch.float32)
     s_col = torch.empty((batch, -(-m // block), n), device=x.device, dtype=torch.float32)
 
@@ -109,7 +116,7 @@ def hip_per_block_quant_dual(
     with torch.cuda.device(x.device):
         rc = L.pcamd_quant_block_dual(
             _lib.ptr(x), _lib.dtype_code(x.dtype), batch, m, n, *xs,
-            _lib.ptr(out_row), _lib.ptr(out_col), _lib.dtype_code(fp8_dtype), *ys,
+            _lib.ptr(out_row), *ys, _lib.ptr(out_col), *yc, _lib.dtype_code(fp8_dtype),
             _lib.ptr(s_row), *s_row.stride(), _lib.ptr(s_col), *s_col.stride(),
             block, float(torch.finfo(fp8_dtype).max), float(eps), _lib.stream_of(x))
     _lib.check(rc, "pcamd_quant_block_dual")

@@ -11,8 +11,9 @@ recipe the reference leaves unfinished (``modules/per_block.py:13-67``):
 * wgrad    ``dW = dY^T X``: dY and X quantized 128x1 (blocks of 128 along
   M, the reduction dimension of this GEMM) from their high-precision values,
   each in the same pass as its 1x128 quantization (``pcamd_quant_block_dual``:
-  one read of X in forward, one of dY in backward; the 128x1 fp8 X is what
-  forward saves);
+  one read of X in forward, one of dY in backward; the 128x1 results are
+  stored transposed, which makes both wgrad operands K-major; the 128x1 fp8
+  X is what forward saves);
 * dbias    ``dY.sum(1)``.
 
 Every GEMM is ``pcamd::block_scaled_bmm``, a ``torch.library`` custom op over
@@ -136,9 +137,10 @@ def _(x, block_m, block_n, fp8_dtype, eps):
 def quant_block_dual(x: torch.Tensor, block: int, fp8_dtype: torch.dtype,
                      eps: float) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
     """``quant_block(x, 1, block)`` and ``quant_block(x, block, 1)`` from one read
-    of x: (fp8 1 x block, its scales [B, M, ceil(N/block)], fp8 block x 1, its
-    scales [B, ceil(M/block), N])."""
-    r, c = hip_per_block_quant_dual(x, block=block, fp8_dtype=fp8_dtype, eps=eps)
+    of x: (fp8 1 x block, its scales [B, M, ceil(N/block)], fp8 block x 1 stored
+    transposed (a [B, N, M] buffer seen as [B, M, N], the K-major operand of a
+    GEMM reducing over M), its scales [B, ceil(M/block), N])."""
+    r, c = hip_per_block_quant_dual(x, block=block, fp8_dtype=fp8_dtype, eps=eps, col_transposed=True)
     return r.tensor, r.dequant_scale, c.tensor, c.dequant_scale
 
 
@@ -146,7 +148,8 @@ def quant_block_dual(x: torch.Tensor, block: int, fp8_dtype: torch.dtype,
 def _(x, block, fp8_dtype, eps):
     b, m, n = x.shape
     return (torch.empty_like(x, dtype=fp8_dtype), x.new_empty((b, m, -(-n // block)), dtype=torch.float32),
-            torch.empty_like(x, dtype=fp8_dtype), x.new_empty((b, -(-m // block), n), dtype=torch.float32))
+            x.new_empty((b, n, m), dtype=fp8_dtype).transpose(-1, -2),
+            x.new_empty((b, -(-m // block), n), dtype=torch.float32))
 
 
 @torch.library.custom_op("pcamd::quant_tensor", mutates_args=())
@@ -245,7 +248,8 @@ class _Float8BlockBMMLinearFunction(torch.autograd.Function):
                 # dX = dY W: A = dY [B,M,N] 1x128 along N; B = W [B,N,K] (N = reduction)
                 grad_input = _block_gemm(qdy, sdy, qw, sw, None, 1, blk, dy.dtype, blk)
             if need_dw:
-                # dW = dY^T X: dY and X (quantized in forward) in 128-row blocks along M
+                # dW = dY^T X: dY and X (quantized in forward) in 128-row blocks along M; from
+                # quant_block_dual both are stored transposed, so A = dY^T and B = X are K-major
                 grad_weight = _block_gemm(qdt.transpose(-2, -1), sdt.transpose(-2, -1), qxm, sxm, None,
                                           1, 1, dy.dtype, blk)
         if ctx.has_bias and ctx.needs_input_grad[2]:

@@ -67,6 +67,7 @@ def test_quantizers_replay(dev):
         "128x128": lambda: hip_per_block_quant(x, block_m=128, block_n=128),
         "128x1": lambda: hip_per_block_quant(x, block_m=128, block_n=1),
         "dual": lambda: hip_per_block_quant_dual(x, block=128),
+        "dual transposed": lambda: hip_per_block_quant_dual(x, block=128, col_transposed=True),
         "channel rows": lambda: hip_per_channel_quant(x3, channel_axis=-2),
         "channel cols": lambda: hip_per_channel_quant(x, channel_axis=-1),
         "tensor": lambda: hip_per_tensor_quant(x),

@@ -239,8 +239,9 @@ DUAL_CASES = [
 ]
 
 
+@pytest.mark.parametrize("col_t", [False, True], ids=["col_rows", "col_transposed"])
 @pytest.mark.parametrize("shape,dtype,block,fmt,kind", DUAL_CASES)
-def test_dual_matches_oracle(dev, shape, dtype, block, fmt, kind):
+def test_dual_matches_oracle(dev, shape, dtype, block, fmt, kind, col_t):
     from practice_cuda_amd.impls.hip_per_block import hip_per_block_quant_dual
     x = make_input(shape, dtype, seed=sum(shape) + block, outliers=0.01 if kind == "outliers" else 0.0)
     if kind == "zero_rows":
@@ -254,8 +255,10 @@ def test_dual_matches_oracle(dev, shape, dtype, block, fmt, kind):
         wide = torch.zeros(*shape[:-1], 640, dtype=x.dtype, device=dev)
         wide[..., :shape[-1]] = xd
         xd = wide[..., :shape[-1]]
-    print(f"dual shape={shape} dtype={dtype} block={block} fmt={fmt} kind={kind}", flush=True)
-    r_row, r_col = hip_per_block_quant_dual(xd, block=block, fp8_dtype=FMT[fmt])
+    print(f"dual shape={shape} dtype={dtype} block={block} fmt={fmt} kind={kind} col_t={col_t}", flush=True)
+    r_row, r_col = hip_per_block_quant_dual(xd, block=block, fp8_dtype=FMT[fmt], col_transposed=col_t)
+    if col_t:
+        assert r_col.tensor.stride(-2) == 1 and r_col.tensor.stride(-1) == shape[-2]
     q1, s1 = O.quant_block(x, 1, block, fmt=fmt)
     q2, s2 = O.quant_block(x, block, 1, fmt=fmt)
     assert r_row.meta["block_m"] == 1 and r_row.meta["block_n"] == block
@@ -279,7 +282,7 @@ def test_dual_full_size(dev):
     m = torch.rand(4096, 7168, generator=g) < 0.001
     x[m] *= 50
     x = x.bfloat16()
-    r_row, r_col = hip_per_block_quant_dual(x.to(dev), block=128)
+    r_row, r_col = hip_per_block_quant_dual(x.to(dev), block=128, col_transposed=True)
     q1, s1 = O.quant_block(x, 1, 128, threads=8)
     assert_same(r_row, q1, s1, "dual 1x128 full size")
     q2, s2 = O.quant_block(x, 128, 1, threads=8)
@@ -292,8 +295,8 @@ def test_dual_rejects_aliased_outputs(dev):
     s1 = torch.empty(128, 1, device=dev)
     s2 = torch.empty(1, 128, device=dev)
     rc = _lib.lib().pcamd_quant_block_dual(
-        _lib.ptr(x), _lib.BF16, 1, 128, 128, 0, 128, 1, _lib.ptr(y), _lib.ptr(y), _lib.E4M3FN,
-        0, 128, 1, _lib.ptr(s1), 0, 1, 1, _lib.ptr(s2), 0, 128, 1, 128, 448.0, 1e-12, _lib.stream_of(x))
+        _lib.ptr(x), _lib.BF16, 1, 128, 128, 0, 128, 1, _lib.ptr(y), 0, 128, 1, _lib.ptr(y), 0, 128, 1,
+        _lib.E4M3FN, _lib.ptr(s1), 0, 1, 1, _lib.ptr(s2), 0, 128, 1, 128, 448.0, 1e-12, _lib.stream_of(x))
     assert rc == -1 and b"alias" in _lib.lib().pcamd_last_error()
 
 
