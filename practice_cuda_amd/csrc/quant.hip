@@ -799,11 +799,17 @@ __global__ __launch_bounds__(kThreads) void colchan_apply_kernel(ColArgs a) {
     if (r < a.m && col_ok) load_chunk<DT>(raw[p], xb + (r * a.sxm + col) * EB);
     else zero_chunk<DT>(raw[p]);
   }
+  // one division per column of the strip (lanes t < 128), shared through LDS
+  __shared__ float qsv[128];
+  if (t < 128) {
+    const int64_t c = strip * 128 + t;
+    const uint32_t* amax_bits = reinterpret_cast<const uint32_t*>(a.scale) + b * a.ssb;
+    qsv[t] = c < a.n ? channel_scales(__uint_as_float(amax_bits[c * a.ssn]), a.fp8_max, a.eps).qs : 0.0f;
+  }
+  __syncthreads();
   float qs[8];
-  const uint32_t* amax_bits = reinterpret_cast<const uint32_t*>(a.scale) + b * a.ssb;
 #pragma unroll
-  for (int i = 0; i < 8; ++i)
-    qs[i] = col_ok ? channel_scales(__uint_as_float(amax_bits[(col + i) * a.ssn]), a.fp8_max, a.eps).qs : 0.0f;
+  for (int i = 0; i < 8; ++i) qs[i] = qsv[lc * 8 + i];
   uint8_t* yb = a.y + b * a.syb;
 #pragma unroll
   for (int p = 0; p < CPT; ++p) {
