@@ -490,10 +490,15 @@ extern "C" int pcamd_bmm_scaled(const void* a, const void* b, int ab_dtype, int6
   hipStream_t st = static_cast<hipStream_t>(stream);
 
   // tuned path: K a multiple of 128, 16-byte aligned operands and rows,
-  // power-of-two block sizes, 32-bit addressable batch slices
+  // power-of-two block sizes, 32-bit addressable batch slices.
+  // PCAMD_BMM_WIDE=0 / PCAMD_BMM_GENERIC select the other kernels (read once)
+  static const bool env_no_wide = [] {
+    const char* e = getenv("PCAMD_BMM_WIDE");
+    return e && e[0] == '0';
+  }();
+  static const bool env_generic = getenv("PCAMD_BMM_GENERIC") != nullptr;
   {
-    const bool wide = k >= 256 && (scale_mode != PCAMD_SCALE_BLOCK || args.qbk == 128) &&
-                      !(getenv("PCAMD_BMM_WIDE") && getenv("PCAMD_BMM_WIDE")[0] == '0');
+    const bool wide = k >= 256 && (scale_mode != PCAMD_SCALE_BLOCK || args.qbk == 128) && !env_no_wide;
     const int64_t TM = wide ? bmm_wide_tile() : bmm_fast_tile_m();
     const int64_t TN = wide ? bmm_wide_tile() : bmm_fast_tile_n();
     const int64_t tm = (m + TM - 1) / TM, tn = (n + TN - 1) / TN;
@@ -506,7 +511,7 @@ extern "C" int pcamd_bmm_scaled(const void* a, const void* b, int ab_dtype, int6
     const bool fast = k > 0 && k % 128 == 0 && args.vec_a && args.vec_b && lda % 16 == 0 && ldb % 16 == 0 &&
                       a_max < (int64_t{1} << 32) - 64 && b_max < (int64_t{1} << 32) - 64 &&
                       m < INT32_MAX && n < INT32_MAX && k < INT32_MAX && tm * tn * batch < INT32_MAX &&
-                      block_ok && getenv("PCAMD_BMM_GENERIC") == nullptr;
+                      block_ok && !env_generic;
     if (fast) {
       FastArgs f{};
       f.a = args.a; f.b = args.b; f.c = c; f.bias = bias; f.sa = sa; f.sb = sb;
