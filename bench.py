@@ -302,6 +302,16 @@ def bench_config5(torch, steps, warmup, dev):
         t = flops / (ms * 1e-3) / 1e12
         res[name] = {"ms": ms, "TFLOP/s": t, "frac_of_fp8_peak": t / FP8_PEAK_TFLOPS}
     total_ms = sum(r["ms"] for r in res.values())
+    # the training layer's wgrad: the same product on K-major operands (its
+    # dual quantizer stores the 128x1 results transposed); not part of the trio
+    dyt_k = QuantResult(dyt.tensor.contiguous(), dyt.dequant_scale, dyt.impl, "block", dict(dyt.meta))
+    qx_mk = QuantResult(qx_m.tensor.transpose(-1, -2).contiguous().transpose(-1, -2), qx_m.dequant_scale,
+                        qx_m.impl, "block", dict(qx_m.meta))
+    ms, _ = graph_time(torch, lambda i: hip_per_block_bmm(dyt_k, qx_mk, out=out_w), steps, warmup)
+    t = flops / (ms * 1e-3) / 1e12
+    res["wgrad_layer_a_k_b_k"] = {"ms": ms, "TFLOP/s": t, "frac_of_fp8_peak": t / FP8_PEAK_TFLOPS,
+                                  "note": "not in the trio total"}
+    del dyt_k, qx_mk
     tflops = 3 * flops / (total_ms * 1e-3) / 1e12
     del qx, qw, qdy, qdy_m, qx_m, wt, dyt, out_f, out_d, out_w, gemms
     torch.cuda.empty_cache()
