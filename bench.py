@@ -312,6 +312,17 @@ def bench_config5(torch, steps, warmup, dev):
     res["wgrad_layer_a_k_b_k"] = {"ms": ms, "TFLOP/s": t, "frac_of_fp8_peak": t / FP8_PEAK_TFLOPS,
                                   "note": "not in the trio total"}
     del dyt_k, qx_mk
+    # the channel-scaled recipe (one scale per row of X and of W) on the forward shape
+    from practice_cuda_amd.impls.hip_per_channel import hip_per_channel_bmm, hip_per_channel_quant
+    cx = hip_per_channel_quant(X[None], channel_axis=-2)
+    cw = hip_per_channel_quant(W[None], channel_axis=-2)
+    cwt = QuantResult(cw.tensor.transpose(-1, -2), cw.dequant_scale, cw.impl, "channel",
+                      {**cw.meta, "channel_axis": -1})
+    ms, _ = graph_time(torch, lambda i: hip_per_channel_bmm(cx, cwt, out=out_f), steps, warmup)
+    t = flops / (ms * 1e-3) / 1e12
+    res["fwd_channel_a_k_b_k"] = {"ms": ms, "TFLOP/s": t, "frac_of_fp8_peak": t / FP8_PEAK_TFLOPS,
+                                  "note": "channel scales (per-channel recipe); not in the trio total"}
+    del cx, cw, cwt
     tflops = 3 * flops / (total_ms * 1e-3) / 1e12
     del qx, qw, qdy, qdy_m, qx_m, wt, dyt, out_f, out_d, out_w, gemms
     torch.cuda.empty_cache()

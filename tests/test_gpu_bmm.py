@@ -262,3 +262,29 @@ def test_exact_small_integers(dev):
 def test_determinism(dev):
     a, b = _fp8((2, 64, 64), 5), _fp8((2, 64, 64), 6)
     assert torch.equal(_tensor_bmm(a, b, 1.0, dev, torch.bfloat16), _tensor_bmm(a, b, 1.0, dev, torch.bfloat16))
+
+
+@pytest.mark.parametrize("layout", ["a_k_b_k", "a_k_b_n"])
+def test_channel_bmm_config5_shape(dev, layout):
+    """Channel-scaled BMM (one scale per row of A, one per column of B) at the
+    config-5 forward shape M=8192, K=4096, N=14336, against an fp32 GEMM of
+    the dequantized operands computed on the GPU (contiguous operands)."""
+    from practice_cuda_amd.impls.hip_per_channel import hip_per_channel_quant
+    g = torch.Generator().manual_seed(5)
+    x = torch.randn(1, 8192, 4096, generator=g).bfloat16().to(dev)
+    w = (torch.randn(1, 14336, 4096, generator=g) * 0.02).bfloat16().to(dev)
+    bmm = get_bmm(f"hip_per_channel_{layout}")
+    qa = hip_per_channel_quant(x, channel_axis=-2)                      # one scale per row of A
+    if layout == "a_k_b_k":                                              # B = W^T, K-major
+        qw = hip_per_channel_quant(w, channel_axis=-2)                  # one scale per row of W
+        qb = QuantResult(qw.tensor.transpose(-1, -2), qw.dequant_scale, qw.impl, "channel",
+                         {**qw.meta, "channel_axis": -1})
+    else:                                                                # B = W^T materialized N-major
+        qb = hip_per_channel_quant(w.transpose(-1, -2).contiguous(), channel_axis=-1)
+    print(f"channel bmm config5 {layout}", flush=True)
+    out = bmm.fn(qa, qb)
+    da = qa.tensor.float() * qa.dequant_scale[..., :, None]
+    db = qb.tensor.float() * qb.dequant_scale[..., None, :]
+    ref = torch.matmul(da.contiguous(), db.contiguous())
+    err = ((out.float() - ref).abs().max() / ref.abs().max()).item()
+    assert err <= TOL, err
