@@ -1,0 +1,78 @@
+"""Seeded random shapes through every quantizer entry point, bit-exact against
+the oracle: ragged and aligned sizes, batches, all three input dtypes, both
+fp8 formats, power-of-two blocks, both channel axes, per-tensor, and the dual
+quantizer with either 128x1 layout. Each case prints its parameters first."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as O
+from practice_cuda_amd.impls.hip_per_block import hip_per_block_quant, hip_per_block_quant_dual
+from practice_cuda_amd.impls.hip_per_channel import hip_per_channel_quant
+from practice_cuda_amd.impls.hip_per_tensor import hip_per_tensor_quant
+
+pytestmark = pytest.mark.gpu
+FMT = {"e4m3": torch.float8_e4m3fn, "e5m2": torch.float8_e5m2}
+DT = {"bf16": torch.bfloat16, "f16": torch.float16, "f32": torch.float32}
+
+
+def _bits(t):
+    return t.contiguous().view(torch.uint8).cpu().numpy()
+
+
+def _sbits(t):
+    return t.detach().float().cpu().numpy().astype(np.float32).reshape(-1).view(np.uint32)
+
+
+def _same(res, q_ref, s_ref, label):
+    assert np.array_equal(_bits(res.tensor), q_ref), f"{label}: fp8 bytes differ"
+    assert np.array_equal(_sbits(res.dequant_scale), np.asarray(s_ref, np.float32).reshape(-1).view(np.uint32)), \
+        f"{label}: scales differ"
+
+
+def _case(i):
+    rng = np.random.default_rng(1000 + i)
+    batch = int(rng.choice([1, 1, 2, 3]))
+    m = int(rng.choice([1, 7, 64, 128, 130, 256, 300, 384, 513]))
+    n = int(rng.choice([8, 24, 128, 136, 256, 520, 1024, 7168, 70]))
+    dtype = str(rng.choice(["bf16", "bf16", "f16", "f32"]))
+    fmt = str(rng.choice(["e4m3", "e4m3", "e5m2"]))
+    op = str(rng.choice(["block", "block", "channel", "tensor", "dual"]))
+    bm = int(rng.choice([1, 1, 16, 128, 2, 64]))
+    bn = int(rng.choice([128, 128, 1, 64, 8, 256]))
+    axis = int(rng.choice([-1, -2]))
+    col_t = bool(rng.integers(0, 2))
+    return dict(batch=batch, m=m, n=n, dtype=dtype, fmt=fmt, op=op, bm=bm, bn=bn, axis=axis, col_t=col_t)
+
+
+@pytest.mark.parametrize("i", range(48))
+def test_random_quantizer_case(dev, i):
+    c = _case(i)
+    print(f"fuzz {i}: {c}", flush=True)
+    g = torch.Generator().manual_seed(i)
+    shape = (c["batch"], c["m"], c["n"]) if c["batch"] > 1 else (c["m"], c["n"])
+    x = torch.randn(*shape, generator=g) * float(np.exp(np.random.default_rng(i).uniform(-6, 3)))
+    x.view(-1)[:: max(1, x.numel() // 7)] *= 40.0          # a few outliers
+    x = x.to(DT[c["dtype"]])
+    xd, f8 = x.to(dev), FMT[c["fmt"]]
+    if c["op"] == "block":
+        r = hip_per_block_quant(xd, block_m=c["bm"], block_n=c["bn"], fp8_dtype=f8)
+        q, s = O.quant_block(x, c["bm"], c["bn"], c["fmt"], threads=4)
+        _same(r, q, s, f"block {c['bm']}x{c['bn']}")
+    elif c["op"] == "channel":
+        r = hip_per_channel_quant(xd, channel_axis=c["axis"], fp8_dtype=f8)
+        q, s = O.quant_channel(x, c["axis"], c["fmt"], threads=4)
+        _same(r, q, s, f"channel {c['axis']}")
+    elif c["op"] == "tensor":
+        r = hip_per_tensor_quant(xd, fp8_dtype=f8)
+        q, ds, _ = O.quant_tensor(x, c["fmt"])
+        assert np.array_equal(_bits(r.tensor), q), "tensor: fp8 bytes differ"
+        assert np.array_equal(_sbits(r.dequant_scale), np.asarray([ds], np.float32).view(np.uint32))
+    else:
+        r_row, r_col = hip_per_block_quant_dual(xd, block=128, fp8_dtype=f8, col_transposed=c["col_t"])
+        q1, s1 = O.quant_block(x, 1, 128, c["fmt"], threads=4)
+        q2, s2 = O.quant_block(x, 128, 1, c["fmt"], threads=4)
+        _same(r_row, q1, s1, "dual 1x128")
+        _same(r_col, q2, s2, "dual 128x1")
