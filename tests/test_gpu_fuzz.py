@@ -76,3 +76,31 @@ def test_random_quantizer_case(dev, i):
         q2, s2 = O.quant_block(x, 128, 1, c["fmt"], threads=4)
         _same(r_row, q1, s1, "dual 1x128")
         _same(r_col, q2, s2, "dual 128x1")
+
+
+def _bmm_case(i):
+    from test_gpu_bmm import LAYOUTS, SCHEMES
+    rng = np.random.default_rng(5000 + i)
+    c = dict(scheme=str(rng.choice(SCHEMES)), layout=str(rng.choice(LAYOUTS)), b=int(rng.choice([1, 2])),
+             m=int(rng.choice([1, 33, 128, 200, 256, 384, 520, 640])),
+             n=int(rng.choice([16, 47, 128, 256, 300, 512, 640])),
+             k=int(rng.choice([128, 256, 384, 512, 65, 200])))
+    if c["layout"].startswith("a_m") and c["m"] == 1:
+        # a single row is contiguous along K as well: the reference's layout check
+        # (fp8_bench/impls/triton_per_block.py:45-53) reads it as k-major and rejects it here
+        c["m"] = 2
+    return c
+
+
+@pytest.mark.parametrize("i", range(24))
+def test_random_bmm_case(dev, i):
+    """Seeded random shapes, schemes and layouts through the registered BMMs,
+    within max-abs-rel 1e-2 of the fp64 product of the dequantized operands."""
+    from test_gpu_bmm import TOL, rand, run_registered
+    c = _bmm_case(i)
+    print(f"bmm fuzz {i}: {c}", flush=True)
+    out, ref = run_registered(f"{c['scheme']}_{c['layout']}", rand((c["b"], c["m"], c["k"]), 100 + i),
+                              rand((c["b"], c["k"], c["n"]), 200 + i), dev)
+    assert out.shape == (c["b"], c["m"], c["n"])
+    err = O.max_abs_rel(out.float().cpu().numpy(), ref)
+    assert err <= TOL, f"max_abs_rel {err}"
