@@ -58,9 +58,10 @@ def block_scaled_bmm(
     """``C[b] = sum_kq (A[b, :, kq] @ B[b, kq, :]) * sa[b, m/qbm, kq] * sb[b, kq, n/qbn] (+ bias)``.
 
     a: fp8 [B, M, K] contiguous along K or M; b: fp8 [B, K, N] contiguous
-    along N or K; sa: fp32 [B, ceil(M/qbm), K/qbk]; sb: fp32
-    [B, K/qbk, ceil(N/qbn)] (any strides); bias: [B, N] (broadcast over M) or
-    None. qbk must be a multiple of 128 dividing K.
+    along N or K; sa: fp32 [B, ceil(M/qbm), ceil(K/qbk)]; sb: fp32
+    [B, ceil(K/qbk), ceil(N/qbn)] (any strides); bias: [B, N] (broadcast over
+    M) or None. qbk must be a multiple of 128; a last, partial K block is
+    scaled like the others (its quantization covered the same columns).
     """
     batch, m, k = a.shape
     n = b.shape[2]
@@ -68,10 +69,10 @@ def block_scaled_bmm(
         raise ValueError(f"incompatible BMM shapes: A={tuple(a.shape)}, B={tuple(b.shape)}")
     if a.dtype not in _FP8 or b.dtype != a.dtype:
         raise ValueError(f"A and B must share an fp8 dtype, got {a.dtype} and {b.dtype}")
-    if qbk % 128 or k % qbk:
-        raise ValueError(f"quant block K ({qbk}) must be a multiple of 128 dividing K ({k})")
-    want_a = (batch, -(-m // qbm), k // qbk)
-    want_b = (batch, k // qbk, -(-n // qbn))
+    if qbk <= 0 or qbk % 128:
+        raise ValueError(f"quant block K ({qbk}) must be a positive multiple of 128")
+    want_a = (batch, -(-m // qbm), -(-k // qbk))
+    want_b = (batch, -(-k // qbk), -(-n // qbn))
     if tuple(sa.shape) != want_a or tuple(sb.shape) != want_b:
         raise ValueError(f"scale shapes must be {want_a} and {want_b}, got {tuple(sa.shape)} and {tuple(sb.shape)}")
     if sa.dtype != torch.float32 or sb.dtype != torch.float32:

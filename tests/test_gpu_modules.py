@@ -45,9 +45,13 @@ def _layer(b, k, n, dev, config, bias=True, seed=0):
     return layer
 
 
-@pytest.mark.parametrize("shape", [(2, 256, 384, 512), (1, 384, 256, 128), (3, 128, 128, 256)])
+@pytest.mark.parametrize("shape", [(2, 256, 384, 512), (1, 384, 256, 128), (3, 128, 128, 256),
+                                   (2, 200, 256, 384), (1, 130, 200, 256)])
 def test_block_recipe_gemms_match_oracle(dev, shape):
-    b, m, k, n = shape  # M, K and N in whole 128 blocks (each is some GEMM's reduction)
+    # M, K and N are each some GEMM's reduction; the last two shapes have ragged
+    # M (wgrad's: the dual quantizer's transposed 128x1 output then takes the
+    # two-quantizer path) and ragged K (partial last quant-K blocks)
+    b, m, k, n = shape
     print(f"block recipe {shape}", flush=True)
     layer = _layer(b, k, n, dev, Float8BlockBMMLinearConfig())
     g = torch.Generator().manual_seed(1)
