@@ -12,9 +12,10 @@ in HBM before the timed region starts.
 
 ``components`` reports the other BASELINE configs the same way (1x128 quant,
 128x128 quant, config 2's weight with one scale per column, the block-scaled
-BMM of config 4 and the config-5 GEMM trio). ``cpu_baseline`` times the CPU
-restatement of the same quantizer (oracle/, OpenMP over rows) on the host
-cores, and the reference's eager-PyTorch form of it.
+BMM of config 4 and the config-5 GEMM trio). ``cpu_baseline`` times the
+reference's PyTorch CPU path on the host cores: the eager form of the same
+quantizer (the lead value), the oracle's C restatement (OpenMP) beside it,
+and fp32 torch.bmm / torch.mm of dequantized operands for configs 4 and 5.
 """
 from __future__ import annotations
 
@@ -372,12 +373,47 @@ def layer_step(torch, X, W, dY, steps, dev):
 
 
 # ---------------------------------------------------------------------------
-# CPU baseline: the oracle's OpenMP restatement of the same quantizer
+# CPU baseline: the reference's PyTorch CPU path on the host cores
 # ---------------------------------------------------------------------------
-def cpu_baseline(torch, x_cpu):
+def host_cpu():
+    """(threads to use, facts about the host). The thread count is the
+    process's CPU share: OMP_NUM_THREADS when the host sets it (the GPU boxes
+    here set it to the cores granted per GPU), else every core this process
+    may run on."""
+    model = None
+    try:
+        with open("/proc/cpuinfo") as fh:
+            for line in fh:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    try:
+        usable = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        usable = os.cpu_count() or 1
+    env = os.environ.get("OMP_NUM_THREADS", "")
+    threads = max(1, min(int(env), usable)) if env.isdigit() and int(env) > 0 else usable
+    return threads, {"os_cpu_count": os.cpu_count(), "usable_cpus": usable, "cpu_model": model,
+                     "omp_num_threads_env": env or None,
+                     "threads_rule": "OMP_NUM_THREADS if set (the host's per-GPU CPU share), "
+                                     "else every usable core"}
+
+
+def cpu_baseline(torch, x_cpu, dev):
+    """The lead value is the reference's PyTorch form of the headline
+    quantizer (kernels/quant/per_channel.py:9-29, fp32 math) run eagerly on
+    the host cores over the full config-2 tensor. Beside it: the oracle's C
+    restatement with OpenMP, BASELINE configs[0] (1x128 groups, eager
+    PyTorch), and the BMM configs through the reference's kernel_reference
+    (fp8_training/fp8_bench/bench_bmm.py:414-416: fp32 torch.bmm / torch.mm of
+    the dequantized operands)."""
     from oracle import oracle as O
-    threads = min(os.cpu_count() or 1, 16)
+    threads, host = host_cpu()
+    torch.set_num_threads(threads)
     sample = x_cpu.contiguous()                 # the full workload tensor
+    lead = torch_eager_baseline(torch, sample, threads)
     O.quant_channel(sample[:64], -2, threads=threads)   # warm (page-in, thread pool)
     times = []
     for _ in range(5):
@@ -387,12 +423,85 @@ def cpu_baseline(torch, x_cpu):
     t = statistics.median(times)
     m, n = sample.shape
     nbytes = m * n * 3 + m * 4
-    return {"value": nbytes / t / 1e9, "unit": "GB/s", "cores": threads, "kind": "port",
-            "sample": f"bf16 [{m},{n}] (the full workload tensor), "
-                      f"median of 5 runs of oracle/fp8_oracle.c per-channel quant, "
-                      f"{threads} OpenMP threads, {t * 1e3:.1f} ms/run",
-            "torch_eager": torch_eager_baseline(torch, sample, threads),
-            "config0": config0_baseline(torch, threads)}
+    oracle_c = {"value": nbytes / t / 1e9, "unit": "GB/s", "threads": threads,
+                "sample": f"bf16 [{m},{n}], median of 5 runs of oracle/fp8_oracle.c per-row quant "
+                          f"(OpenMP), {t * 1e3:.1f} ms/run"}
+    torch.set_num_threads(threads)  # the oracle call sets the process's OpenMP thread count too
+    out = {"value": lead["value"], "unit": "GB/s", "cores": torch.get_num_threads(), "kind": "port",
+           "sample": lead["sample"], "matches_oracle": lead["matches_oracle"], "host": host,
+           "torch_threads": torch.get_num_threads(), "oracle_c": oracle_c,
+           "config0": config0_baseline(torch, threads)}
+    torch.set_num_threads(threads)
+    out["config4_bmm"] = cpu_bmm_config4(torch, dev)
+    out["config5_gemms"] = cpu_gemms_config5(torch, dev)
+    return out
+
+
+def cpu_bmm_config4(torch, dev):
+    """BASELINE config 4 through kernel_reference on the host cores: fp32
+    torch.bmm of the dequantized [128,2048,128] x [128,128,512] operands
+    (quantized by this build's kernels on the GPU, then copied over), 1 warmup
+    and the median of 3 runs; checked against the GPU kernel's output."""
+    from practice_cuda_amd.impls.hip_per_block import hip_per_block_bmm, hip_per_block_quant
+    g = torch.Generator().manual_seed(0)
+    ah = torch.randn(128, 2048, 128, generator=g).bfloat16()
+    bh = torch.randn(128, 128, 512, generator=g).bfloat16()
+    qa = hip_per_block_quant(ah.to(dev), block_m=1, block_n=128)
+    qb = hip_per_block_quant(bh.to(dev), block_m=128, block_n=128)
+    gpu = hip_per_block_bmm(qa, qb).float().cpu()
+    a, b = qa.dequantize().cpu(), qb.dequantize().cpu()
+    ref = torch.bmm(a, b)
+    times = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        torch.bmm(a, b)
+        times.append(time.perf_counter() - t0)
+    t = statistics.median(times)
+    flops = 2 * 128 * 2048 * 512 * 128
+    err = ((gpu - ref).abs().max() / ref.abs().max()).item()
+    return {"value": flops / t / 1e12, "unit": "TFLOP/s", "ms": t * 1e3, "threads": torch.get_num_threads(),
+            "gpu_max_abs_rel": err,
+            "sample": "the full config-4 product, fp32 torch.bmm of dequantized operands, median of 3 runs"}
+
+
+def cpu_gemms_config5(torch, dev):
+    """The config-5 GEMM trio through kernel_reference on the host cores: three
+    fp32 torch.mm of dequantized operands at M=8192 K=4096 N=14336, one run
+    each (about a second per GEMM on 16 cores), each checked against the GPU
+    kernel's output."""
+    from practice_cuda_amd.impls.hip_per_block import hip_per_block_bmm, hip_per_block_quant
+    from practice_cuda_amd.registry import QuantResult
+    M, K, N = 8192, 4096, 14336
+    g = torch.Generator().manual_seed(0)
+    X = torch.randn(M, K, generator=g).bfloat16().to(dev)[None]
+    W = (torch.randn(N, K, generator=g) * 0.02).bfloat16().to(dev)[None]
+    dY = (torch.randn(M, N, generator=g) * 1e-3).bfloat16().to(dev)[None]
+
+    def tr(q):
+        return QuantResult(q.tensor.transpose(-1, -2), q.dequant_scale.transpose(-1, -2), q.impl, "block",
+                           {**q.meta, "block_m": q.meta["block_n"], "block_n": q.meta["block_m"]})
+
+    qx = hip_per_block_quant(X, block_m=1, block_n=128)
+    qw = hip_per_block_quant(W, block_m=128, block_n=128)
+    qdy = hip_per_block_quant(dY, block_m=1, block_n=128)
+    qdy_m = hip_per_block_quant(dY, block_m=128, block_n=1)
+    qx_m = hip_per_block_quant(X, block_m=128, block_n=1)
+    cases = {"fwd": (qx, tr(qw)), "dgrad": (qdy, qw), "wgrad": (tr(qdy_m), qx_m)}
+    res, total = {}, 0.0
+    for name, (qa, qb) in cases.items():
+        gpu = hip_per_block_bmm(qa, qb)[0].float().cpu()
+        a = qa.dequantize()[0].contiguous().cpu()
+        b = qb.dequantize()[0].contiguous().cpu()
+        t0 = time.perf_counter()
+        ref = torch.mm(a, b)
+        t = time.perf_counter() - t0
+        total += t
+        err = ((gpu - ref).abs().max() / ref.abs().max()).item()
+        res[name] = {"ms": t * 1e3, "TFLOP/s": 2 * M * N * K / t / 1e12, "gpu_max_abs_rel": err}
+        del gpu, a, b, ref
+    return {"value": 3 * 2 * M * N * K / total / 1e12, "unit": "TFLOP/s", "threads": torch.get_num_threads(),
+            "gemms": res, "sample": "fwd, dgrad and wgrad at the full config-5 shape, fp32 torch.mm of "
+                                    "dequantized operands, one run each"}
 
 
 def torch_channel_quant(torch, x, fp8_max=448.0, eps=1e-12):
@@ -570,7 +679,7 @@ def main():
         line["components"] = comps
 
     if not args.no_cpu_baseline:
-        line["cpu_baseline"] = cpu_baseline(torch, x2)
+        line["cpu_baseline"] = cpu_baseline(torch, x2, dev)
     print(json.dumps(line))
 
 

@@ -153,15 +153,6 @@ int pcamd_bmm_scaled(const void *a, const void *b, int ab_dtype,
                      int scales_are_quant, int64_t qbm, int64_t qbk,
                      int64_t qbn, int activation, void *stream);
 
-/*
- * Device self-test of the fp32 -> fp8 conversion used by the quantizers:
- * compares the gfx950 hardware conversion with an integer restatement of
- * round-to-nearest-even over every fp32 bit pattern with |x| <= fp8 max.
- * result (device, 4 x uint32) receives {mismatches, first mismatching
- * pattern, checked count low 32 bits, 0}. fmt is PCAMD_E4M3FN or PCAMD_E5M2.
- */
-int pcamd_selftest_fp8_convert(int fmt, uint32_t *result, void *stream);
-
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,32 @@
+/*
+ * pcamd_fp8_selftest.h - test-only entry point of libpcamd_fp8.so.
+ *
+ * Not part of the product interface (include/pcamd_fp8.h): the test suite
+ * calls it to pin the hardware fp8 conversion the quantizers use. It has no
+ * counterpart in the reference (xuOAO/practice_cuda), whose fp8 casts are
+ * Triton's `.to(fp8)` (fp8_training/fp8_bench/kernels/quant/per_block.py:47).
+ */
+#ifndef PCAMD_FP8_SELFTEST_H
+#define PCAMD_FP8_SELFTEST_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/*
+ * Device self-test of the fp32 -> fp8 conversion used by the quantizers:
+ * compares the gfx950 hardware conversion with an integer restatement of
+ * round-to-nearest-even over every fp32 bit pattern with |x| <= fp8 max.
+ * result (device, 4 x uint32) receives {mismatches, first mismatching
+ * pattern, checked count low 32 bits, 0}. fmt is PCAMD_E4M3FN (3) or
+ * PCAMD_E5M2 (4). Returns 0 or a negative status (see pcamd_fp8.h).
+ */
+int pcamd_selftest_fp8_convert(int fmt, uint32_t *result, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* PCAMD_FP8_SELFTEST_H */

@@ -1,4 +1,5 @@
-"""ctypes binding of libpcamd_fp8.so (the C ABI declared in include/pcamd_fp8.h).
+"""ctypes binding of libpcamd_fp8.so (the C ABI declared in include/pcamd_fp8.h,
+plus the test-only include/pcamd_fp8_selftest.h).
 
 The library must have been built (``python -m practice_cuda_amd.build`` or
 ``__graft_entry__.build()``). There is no fallback: if it is missing every
@@ -37,8 +38,9 @@ EXPORTED_SYMBOLS = (
     "pcamd_quant_channel",
     "pcamd_quant_tensor",
     "pcamd_bmm_scaled",
-    "pcamd_selftest_fp8_convert",
 )
+# test-only entry points (include/pcamd_fp8_selftest.h), exported by the same library
+TEST_SYMBOLS = ("pcamd_selftest_fp8_convert",)
 
 _i64 = ctypes.c_int64
 _int = ctypes.c_int

@@ -28,12 +28,18 @@ int check_launch(const char* what) {
   return PCAMD_OK;
 }
 
-int device_cu_count() {
+int stream_device(hipStream_t st) {
+  int dev = -1;
+  if (st == nullptr) return hipGetDevice(&dev) == hipSuccess ? dev : -1;
+  return hipStreamGetDevice(st, &dev) == hipSuccess ? dev : -1;
+}
+
+int device_cu_count(hipStream_t st) {
   constexpr int kMaxDevices = 64;
   static std::atomic<int> cache[kMaxDevices];  // 0: not queried yet
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess) return 0;
-  const bool cached = dev >= 0 && dev < kMaxDevices;
+  const int dev = stream_device(st);
+  if (dev < 0) return 0;
+  const bool cached = dev < kMaxDevices;
   if (cached) {
     const int c = cache[dev].load(std::memory_order_relaxed);
     if (c > 0) return c;
@@ -42,6 +48,23 @@ int device_cu_count() {
   if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
   if (cached && n > 0) cache[dev].store(n, std::memory_order_relaxed);
   return n;
+}
+
+int ensure_dynamic_lds(const void* kern, int bytes, hipStream_t st, std::atomic<uint64_t>& done) {
+  const int dev = stream_device(st);
+  if (dev < 0) return set_error(PCAMD_ERR_LAUNCH, "cannot determine the stream's device");
+  const uint64_t bit = dev < 64 ? uint64_t{1} << dev : 0;
+  if (bit && (done.load(std::memory_order_acquire) & bit)) return PCAMD_OK;
+  int cur = -1;
+  if (hipGetDevice(&cur) != hipSuccess) return set_error(PCAMD_ERR_LAUNCH, "hipGetDevice failed");
+  if (cur != dev && hipSetDevice(dev) != hipSuccess)
+    return set_error(PCAMD_ERR_LAUNCH, "hipSetDevice(%d) failed", dev);
+  const hipError_t e = hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+  if (cur != dev) (void)hipSetDevice(cur);
+  if (e != hipSuccess) return set_error(PCAMD_ERR_LAUNCH, "hipFuncSetAttribute: %s", hipGetErrorString(e));
+  // concurrent first calls may both set the attribute: the call is idempotent
+  if (bit) done.fetch_or(bit, std::memory_order_acq_rel);
+  return PCAMD_OK;
 }
 
 }  // namespace pcamd

@@ -565,13 +565,9 @@ int launch_single(const FastArgs& a, hipStream_t st) {
 template <bool A_K, bool B_K, int FMT, int MODE, bool SB_COL, bool QB1>
 int launch_one(const FastArgs& a, hipStream_t st) {
   auto kern = bmm_fast_kernel<A_K, B_K, FMT, MODE, SB_COL, QB1>;
-  static bool configured = false;  // benign race: the attribute call is idempotent
-  if (!configured) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, 2 * STAGE);
-    if (e != hipSuccess) return set_error(PCAMD_ERR_LAUNCH, "hipFuncSetAttribute: %s", hipGetErrorString(e));
-    configured = true;
-  }
+  static std::atomic<uint64_t> configured{0};  // devices whose LDS limit is set
+  const int rc = ensure_dynamic_lds(reinterpret_cast<const void*>(kern), 2 * STAGE, st, configured);
+  if (rc != 0) return rc;
   kern<<<a.total_tiles, NT, 2 * STAGE, st>>>(a);
   return check_launch("bmm_fast_kernel");
 }

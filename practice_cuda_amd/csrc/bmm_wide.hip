@@ -557,13 +557,9 @@ constexpr int LDS_BYTES = 2 * STAGE + 2 * (BM + BN) * 4;
 template <bool A_K, bool B_K, int FMT, int MODE, int SBK, int JN>
 int launch_tiles(const FastArgs& a, int grid, hipStream_t st) {
   auto kern = bmm_wide_kernel<A_K, B_K, FMT, MODE, SBK, JN>;
-  static bool configured = false;  // benign race: the attribute call is idempotent
-  if (!configured) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, LDS_BYTES);
-    if (e != hipSuccess) return set_error(PCAMD_ERR_LAUNCH, "hipFuncSetAttribute: %s", hipGetErrorString(e));
-    configured = true;
-  }
+  static std::atomic<uint64_t> configured{0};  // devices whose LDS limit is set
+  const int rc = ensure_dynamic_lds(reinterpret_cast<const void*>(kern), LDS_BYTES, st, configured);
+  if (rc != 0) return rc;
   kern<<<grid, NT, LDS_BYTES, st>>>(a);
   return check_launch("bmm_wide_kernel");
 }
@@ -573,7 +569,7 @@ int launch_tiles(const FastArgs& a, int grid, hipStream_t st) {
 // runs as a second launch of half tiles instead.
 template <bool A_K, bool B_K, int FMT, int MODE, int SBK>
 int launch_one(const FastArgs& a, hipStream_t st) {
-  const int cus = device_cu_count();
+  const int cus = device_cu_count(st);
   const int tail = cus > 0 && a.total_tiles > cus ? a.total_tiles % cus : 0;
   if (tail == 0 || 2 * tail > cus) return launch_tiles<A_K, B_K, FMT, MODE, SBK, 8>(a, a.total_tiles, st);
   FastArgs whole = a;

@@ -1457,10 +1457,10 @@ extern "C" int pcamd_quant_tensor(const void* x, int x_dtype, int64_t batch, int
 extern "C" int pcamd_selftest_fp8_convert(int fmt, uint32_t* result, void* stream) {
   clear_error();
   if (!result) return set_error(PCAMD_ERR_INVALID, "null result pointer");
+  if (fmt != kE4M3 && fmt != kE5M2) return set_error(PCAMD_ERR_INVALID, "unknown fp8 format %d", fmt);
   hipStream_t st = static_cast<hipStream_t>(stream);
   selftest_init_kernel<<<1, 1, 0, st>>>(result);
   if (fmt == kE4M3) selftest_convert_kernel<kE4M3><<<4096, kThreads, 0, st>>>(result, 0x43E00000u);
-  else if (fmt == kE5M2) selftest_convert_kernel<kE5M2><<<4096, kThreads, 0, st>>>(result, 0x47600000u);
-  else return set_error(PCAMD_ERR_INVALID, "unknown fp8 format %d", fmt);
+  else selftest_convert_kernel<kE5M2><<<4096, kThreads, 0, st>>>(result, 0x47600000u);
   return check_launch("selftest_convert_kernel");
 }

@@ -126,6 +126,40 @@ def hip_per_channel_bmm(
         _lib.SCALE_CHANNEL, False, 1, 128, 1, activation, batch, m, n, k)
 
 
+def hip_torch_compile_role_quant(
+    x: torch.Tensor,
+    *,
+    channel_axis: int = -1,
+    fp8_dtype: torch.dtype = torch.float8_e4m3fn,
+    eps: float = 1e-12,
+    profile: bool = False,
+) -> QuantResult:
+    """The reference's ``torch_compile_per_channel`` entry
+    (fp8_training/fp8_bench/impls/triton_per_channel.py:54-87, math at
+    kernels/quant/per_channel.py:9-29), served by the HIP per-channel kernel:
+    the same arguments, the same two checks before anything runs (rank,
+    channel_axis), and the result fields that entry returns (impl name,
+    ``quant_strategy: "torch_compile"``). Scales are the per-channel ones,
+    ds = max(amax, eps) / fp8_max; the quant scale is the true quotient
+    fp8_max / s, as in the Triton kernels (the compiled form evaluates it as
+    reciprocal(s) * fp8_max, which can differ in its last bit)."""
+    del profile
+    if x.ndim not in (2, 3):
+        raise ValueError(f"per-channel quant expects a 2D or 3D tensor, got {tuple(x.shape)}")
+    if channel_axis not in (-1, -2):
+        raise ValueError(f"channel_axis must be -1 or -2, got {channel_axis}")
+    q = hip_per_channel_quant(x, channel_axis=channel_axis, fp8_dtype=fp8_dtype, eps=eps)
+    q.impl = "torch_compile_per_channel"
+    q.meta["quant_strategy"] = "torch_compile"
+    return q
+
+
+register_quant(
+    "torch_compile_per_channel",
+    hip_torch_compile_role_quant,
+    "The reference's torch.compile per-channel entry, run by the HIP per-channel kernel; "
+    "E4M3 and E5M2.",
+)
 register_quant(
     "hip_per_channel_one_pass",
     partial(hip_per_channel_quant, one_pass=True),

@@ -11,12 +11,14 @@ import pytest
 
 from practice_cuda_amd import _lib
 
-HEADER = os.path.join(os.path.dirname(os.path.dirname(__file__)), "include", "pcamd_fp8.h")
+INCLUDE = os.path.join(os.path.dirname(os.path.dirname(__file__)), "include")
+HEADER = os.path.join(INCLUDE, "pcamd_fp8.h")
+TEST_HEADER = os.path.join(INCLUDE, "pcamd_fp8_selftest.h")
 FAKE = ctypes.c_void_p(0x10000)  # never dereferenced: validation fails first
 
 
-def declared_functions() -> list[str]:
-    text = open(HEADER).read()
+def declared_functions(path: str = HEADER) -> list[str]:
+    text = open(path).read()
     return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\s*\*?\s*(pcamd_\w+)\s*\(", text, re.M)))
 
 
@@ -27,6 +29,17 @@ def test_library_exports_header_symbols():
     for name in names:
         assert hasattr(L, name), f"{name} declared in the header but not exported"
     assert sorted(_lib.EXPORTED_SYMBOLS) == names
+
+
+def test_test_only_symbols_live_in_their_own_header():
+    L = _lib.lib()
+    names = declared_functions(TEST_HEADER)
+    assert names == sorted(_lib.TEST_SYMBOLS)
+    assert not set(names) & set(declared_functions())
+    for name in names:
+        assert hasattr(L, name)
+    assert L.pcamd_selftest_fp8_convert(7, FAKE, None) == -1
+    assert b"fp8 format" in L.pcamd_last_error()
 
 
 def test_abi_version_matches_header():

@@ -402,3 +402,19 @@ def test_dequant_roundtrip(dev):
               hip_per_tensor_quant(x)):
         xh = r.dequantize()
         assert torch.allclose(xh, x, rtol=1e-1, atol=0.05 * x.abs().max().item())
+
+
+@pytest.mark.parametrize("axis", [-1, -2])
+def test_torch_compile_role_same_bytes(dev, axis):
+    """The registry's torch_compile_per_channel entry runs the per-channel
+    kernel: bytes and scales identical to hip_per_channel, the reference's
+    result fields for that entry (impl name, quant_strategy)."""
+    from practice_cuda_amd import get_quant
+    g = torch.Generator().manual_seed(11)
+    x = torch.randn(3, 96, 160, generator=g).bfloat16().to(dev)
+    a = get_quant("torch_compile_per_channel").fn(x, channel_axis=axis)
+    b = get_quant("hip_per_channel").fn(x, channel_axis=axis)
+    assert torch.equal(a.tensor.view(torch.uint8), b.tensor.view(torch.uint8))
+    assert torch.equal(a.dequant_scale, b.dequant_scale)
+    assert a.impl == "torch_compile_per_channel" and a.meta["quant_strategy"] == "torch_compile"
+    assert a.granularity == "channel" and a.meta["channel_axis"] == axis

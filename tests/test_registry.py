@@ -22,7 +22,7 @@ FP8 = torch.float8_e4m3fn
 def test_builtin_names():
     R.load_builtin_impls()
     for name in ("hip_per_block_1d", "hip_per_block_2d", "hip_per_channel",
-                 "hip_per_channel_one_pass", "hip_per_tensor"):
+                 "hip_per_channel_one_pass", "hip_per_tensor", "torch_compile_per_channel"):
         assert name in R.QUANT_IMPLS
     layouts = ("a_k_b_k", "a_k_b_n", "a_k_b_n_transpose", "a_m_b_n", "a_m_transpose_b_n_transpose")
     names = R.bmm_impl_names()
@@ -156,3 +156,12 @@ def test_bmm_validation_errors():
     tb = _qr((2, 256, 96), "tensor", {}, ())
     with pytest.raises(ValueError, match="one combined dequant scale"):
         hip_per_tensor_bmm(ta, tb, dequant_scale=torch.ones(2))
+
+
+def test_torch_compile_role_checks_before_launch():
+    # impls/triton_per_channel.py:63-68: rank, then channel_axis, both ValueError
+    fn = R.get_quant("torch_compile_per_channel").fn
+    with pytest.raises(ValueError, match="2D or 3D"):
+        fn(torch.zeros(4, dtype=torch.bfloat16))
+    with pytest.raises(ValueError, match="channel_axis must be -1 or -2"):
+        fn(torch.zeros(4, 4, dtype=torch.bfloat16), channel_axis=0)
