@@ -17,6 +17,8 @@
  *                          (launches kernels/quant/per_channel.py:35-102, :105-267)
  *   pcamd_quant_tensor  <- fp8_training/fp8_bench/impls/triton_per_tensor.py:28-95
  *                          and kernels/fp8_bmm/fp8_warper.py:9-77
+ *   pcamd_bmm_quant_a   <- kernels/fp8_bmm/kernel/fp8_quant_bmm_fused_kernel.py:30-146
+ *                          (its intent: the activation quantized inside the GEMM)
  *   pcamd_bmm_scaled    <- impls/triton_per_block.py:232-420 (block scales),
  *                          impls/triton_per_channel.py:271-427 (channel scales),
  *                          impls/triton_per_tensor.py:140-306 and
@@ -152,6 +154,35 @@ int pcamd_bmm_scaled(const void *a, const void *b, int ab_dtype,
                      int64_t ssbb, int64_t ssb1, int64_t ssb2, int scale_mode,
                      int scales_are_quant, int64_t qbm, int64_t qbk,
                      int64_t qbn, int activation, void *stream);
+
+/*
+ * Block-scaled FP8 GEMM with the activation quantization fused into the K
+ * loop: a (bf16 or fp16, [batch, m, k], contiguous along k with 16-byte
+ * aligned rows) is quantized in 1 x 128 groups along k inside the kernel -
+ * bytes and dequant scales exactly those of pcamd_quant_block(block_m = 1,
+ * block_n = 128, fp8_max, eps) into ab_dtype - and multiplied by the fp8 b
+ * (block scales sb[b, k/128, n/qbn], quant-K block 128) as pcamd_bmm_scaled
+ * would with those A scales. qa_out / sa_out (both or neither; qa_out
+ * contiguous along k, 8-byte aligned rows) receive the quantized A and its
+ * scales [batch, m, k/128]. k must be a positive multiple of 128; other
+ * layouts return PCAMD_ERR_UNSUPPORTED (quantize, then pcamd_bmm_scaled).
+ * Replaces the intent of the reference's fused quant + BMM kernel
+ * (kernels/fp8_bmm/kernel/fp8_quant_bmm_fused_kernel.py:30-146), whose
+ * per-tile scale helper is unfinished there, with the per-block recipe of
+ * fp8_training/fp8_bench/impls/triton_per_block.py:60-150 (A) and :232-420
+ * (GEMM).
+ */
+int pcamd_bmm_quant_a(const void *a, int a_dtype, const void *b, int ab_dtype,
+                      int64_t batch, int64_t m, int64_t n, int64_t k,
+                      int64_t sab, int64_t sam, int64_t sak, int64_t sbb,
+                      int64_t sbk, int64_t sbn, void *c, int c_dtype,
+                      int64_t scb, int64_t scm, int64_t scn, const void *bias,
+                      int bias_dtype, int64_t sbiasb, int64_t sbiasm,
+                      int64_t sbiasn, const float *sb, int64_t ssbb,
+                      int64_t ssb1, int64_t ssb2, int64_t qbn, void *qa_out,
+                      int64_t sqab, int64_t sqam, int64_t sqak, float *sa_out,
+                      int64_t soab, int64_t soam, int64_t soak, float fp8_max,
+                      float eps, int activation, void *stream);
 
 #ifdef __cplusplus
 }

@@ -538,3 +538,75 @@ extern "C" int pcamd_bmm_scaled(const void* a, const void* b, int ab_dtype, int6
   if (ab_dtype == kE5M2) return bmm::launch_layout<kE5M2>(args, a_k, b_k, mode, st);
   return bmm::launch_layout<kE4M3>(args, a_k, b_k, mode, st);
 }
+
+// Block-scaled BMM with the A operand quantized inside the kernel (1 x 128
+// groups along K, the quantizer's exact bytes and scales); see
+// include/pcamd_fp8.h. Layouts outside the fused kernel's envelope return
+// PCAMD_ERR_UNSUPPORTED so the caller can quantize and multiply separately.
+extern "C" int pcamd_bmm_quant_a(const void* a, int a_dtype, const void* b, int ab_dtype, int64_t batch,
+                                 int64_t m, int64_t n, int64_t k, int64_t sab, int64_t sam, int64_t sak,
+                                 int64_t sbb, int64_t sbk, int64_t sbn, void* c, int c_dtype, int64_t scb,
+                                 int64_t scm, int64_t scn, const void* bias, int bias_dtype, int64_t sbiasb,
+                                 int64_t sbiasm, int64_t sbiasn, const float* sb, int64_t ssbb, int64_t ssb1,
+                                 int64_t ssb2, int64_t qbn, void* qa_out, int64_t sqab, int64_t sqam,
+                                 int64_t sqak, float* sa_out, int64_t soab, int64_t soam, int64_t soak,
+                                 float fp8_max, float eps, int activation, void* stream) {
+  clear_error();
+  if (a_dtype != kBF16 && a_dtype != kF16)
+    return set_error(PCAMD_ERR_INVALID, "A must be bf16 (code %d) or fp16 (code %d), got %d", kBF16, kF16, a_dtype);
+  if (ab_dtype != kE4M3 && ab_dtype != kE5M2)
+    return set_error(PCAMD_ERR_INVALID, "b must be fp8 (code %d or %d), got %d", kE4M3, kE5M2, ab_dtype);
+  if (c_dtype != kF32 && c_dtype != kBF16 && c_dtype != kF16 && c_dtype != kE4M3 && c_dtype != kE5M2)
+    return set_error(PCAMD_ERR_INVALID, "unsupported output dtype code %d", c_dtype);
+  if (bias && bias_dtype != kF32 && bias_dtype != kBF16 && bias_dtype != kF16)
+    return set_error(PCAMD_ERR_INVALID, "unsupported bias dtype code %d", bias_dtype);
+  if (batch < 0 || m < 0 || n < 0 || k < 0) return set_error(PCAMD_ERR_INVALID, "negative size");
+  if (activation != PCAMD_ACT_NONE && activation != PCAMD_ACT_GELU)
+    return set_error(PCAMD_ERR_INVALID, "unknown activation %d", activation);
+  if (!(fp8_max > 0.0f) || !(eps >= 0.0f)) return set_error(PCAMD_ERR_INVALID, "need fp8_max > 0 and eps >= 0");
+  if (qbn <= 0 || (qbn & (qbn - 1))) return set_error(PCAMD_ERR_INVALID, "qbn must be a power of two");
+  if ((qa_out == nullptr) != (sa_out == nullptr))
+    return set_error(PCAMD_ERR_INVALID, "qa_out and sa_out are given together or not at all");
+  if (batch == 0 || m == 0 || n == 0) return PCAMD_OK;
+  if (!c || !sb || (k > 0 && (!a || !b))) return set_error(PCAMD_ERR_INVALID, "null pointer");
+  if (scn != 1) return set_error(PCAMD_ERR_INVALID, "C must be contiguous along N");
+  const bool b_k = sbk == 1;
+  if (!b_k && sbn != 1) return set_error(PCAMD_ERR_INVALID, "B must be contiguous along N or K");
+  // the fused kernel's envelope
+  auto al16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+  const int64_t lda = sam * 2, ldb = b_k ? sbn : sbk;
+  const int64_t tm = (m + bmm_fast_tile_m() - 1) / bmm_fast_tile_m();
+  const int64_t tn = (n + bmm_fast_tile_n() - 1) / bmm_fast_tile_n();
+  const int64_t a_max = (tm * bmm_fast_tile_m()) * lda + k * 2;
+  const int64_t b_max = b_k ? (tn * bmm_fast_tile_n()) * ldb + k : (k - 1) * ldb + tn * bmm_fast_tile_n();
+  const bool ok = k > 0 && k % 128 == 0 && sak == 1 && al16(a) && lda % 16 == 0 && (sab * 2) % 16 == 0 &&
+                  al16(b) && ldb % 16 == 0 && sbb % 16 == 0 && a_max < (int64_t{1} << 32) - 64 &&
+                  b_max < (int64_t{1} << 32) - 64 && m < INT32_MAX && n < INT32_MAX &&
+                  tm * tn * batch < INT32_MAX &&
+                  (!qa_out || (sqak == 1 && sqam % 8 == 0 && sqab % 8 == 0 &&
+                               (reinterpret_cast<uintptr_t>(qa_out) & 7) == 0));
+  if (!ok)
+    return set_error(PCAMD_ERR_UNSUPPORTED,
+                     "fused A quantization needs a K-major 16-byte aligned A, K a positive multiple of 128, "
+                     "an aligned B and 32-bit addressable batch slices");
+  FastArgs f{};
+  f.a = static_cast<const uint8_t*>(a); f.b = static_cast<const uint8_t*>(b); f.c = c; f.bias = bias;
+  f.sa = nullptr; f.sb = sb;
+  f.m = static_cast<int32_t>(m); f.n = static_cast<int32_t>(n); f.k = static_cast<int32_t>(k);
+  f.sab = sab * 2; f.sbb = sbb;
+  f.lda = static_cast<uint32_t>(lda); f.ldb = static_cast<uint32_t>(ldb);
+  f.a_extent = static_cast<uint32_t>(((m - 1) * sam + k) * 2);
+  f.b_extent = static_cast<uint32_t>(b_k ? (n - 1) * sbn + k : (k - 1) * sbk + n);
+  f.scb = scb; f.scm = scm; f.scn = scn;
+  f.sbiasb = sbiasb; f.sbiasm = sbiasm; f.sbiasn = sbiasn;
+  f.ssbb = ssbb; f.ssb1 = ssb1; f.ssb2 = ssb2;
+  f.qbk = 128; f.qbm_shift = 0; f.qbn_shift = bmm::log2_or_neg(qbn);
+  f.tiles_m = static_cast<int32_t>(tm); f.tiles_n = static_cast<int32_t>(tn);
+  f.tiles_per_batch = static_cast<int32_t>(tm * tn);
+  f.total_tiles = static_cast<int32_t>(tm * tn * batch);
+  f.c_dtype = c_dtype; f.bias_dtype = bias_dtype; f.act = activation; f.scales_are_quant = 0;
+  f.qa_out = static_cast<uint8_t*>(qa_out); f.sa_out = sa_out;
+  f.sqab = sqab; f.sqam = sqam; f.soab = soab; f.soam = soam; f.soak = soak;
+  f.fp8_max = fp8_max; f.eps = eps;
+  return bmm_fused_launch(f, a_dtype, ab_dtype, b_k, qbn < 16, static_cast<hipStream_t>(stream));
+}

@@ -27,6 +27,15 @@ struct FastArgs {
   int32_t tiles_m, tiles_n, tiles_per_batch, total_tiles;
   int32_t tile_base;           // first tile of a launch that covers a range of tiles
   int32_t c_dtype, bias_dtype, act, scales_are_quant;
+  // fused A quantization (bmm_fused_launch only): `a` holds 16-bit values
+  // (lda, sab and a_extent in bytes) quantized in the kernel in 1 x 128 groups
+  // with fp8_max / eps; qa_out / sa_out (both or neither) receive the fp8
+  // bytes and dequant scales, written by the workgroups of the first N tile.
+  uint8_t* qa_out;
+  float* sa_out;
+  int64_t sqab, sqam;          // qa_out strides (elements; contiguous along k)
+  int64_t soab, soam, soak;    // sa_out strides (elements)
+  float fp8_max, eps;
 };
 
 // mode: 0 block, 1 channel, 2 tensor
@@ -34,6 +43,12 @@ int bmm_fast_launch(const FastArgs& a, int ab_dtype, bool a_k, bool b_k, int mod
                     hipStream_t st);
 int bmm_fast_tile_m();
 int bmm_fast_tile_n();
+
+// 128 x 256-tile kernel with the A operand quantized inside the K loop:
+// a_dtype PCAMD_BF16 / PCAMD_F16 (K-major, 16-byte aligned rows), block
+// scales on B with quant_block_k == 128 (sb_col: qbn < 16), fmt the fp8 code
+// of B and of the quantized A
+int bmm_fused_launch(const FastArgs& a, int a_dtype, int fmt, bool b_k, bool sb_col, hipStream_t st);
 
 // 256 x 256-tile, 8-wave kernel for two or more K steps (bmm_wide.hip)
 // block mode requires quant_block_k == 128 and power-of-two qbm / qbn

@@ -142,6 +142,47 @@ PCAMD_DEV v8i frag(const uint8_t* tile, int row, int g) {
   return f;
 }
 
+// Fused A quantization: the 128 x 128 A tile of a K step arrives as 16-bit
+// values (bf16 / fp16) in registers and leaves as fp8 in the swizzled LDS
+// layout frag() reads. Lane l of wave w holds, for i = 0..7, chunk l & 15 (8
+// elements) of row 32 w + 4 i + l / 16, so the 16 lanes of a DPP row hold one
+// row's 128-element group: its amax is group_max<16> and its scales and bytes
+// are those of the 1 x 128 quantizer (quant_groups_kernel: the same helpers,
+// the reference's per-block math kernels/quant/per_block.py:35-48).
+template <int DT>
+struct AQStage {
+  uint4 r[8];
+  PCAMD_DEV static int row_of(int wave, int lane, int i) { return wave * 32 + i * 4 + (lane >> 4); }
+  PCAMD_DEV void load(__amdgpu_buffer_rsrc_t rs, uint32_t row0, uint32_t ld, uint32_t k0, int wave, int lane) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      r[i] = buf_load16(rs, (row0 + row_of(wave, lane, i)) * ld + k0 * 2 + (lane & 15) * 16);
+  }
+  // tile: the stage's A region; sa: the stage's 128 row scales in LDS. With
+  // write_out, rows below m also go to qa_out / sa_out (quant-K block kb).
+  template <int FMT>
+  PCAMD_DEV void store(uint8_t* tile, float* sa, const FastArgs& a, int bidx, int m0, int kb, bool write_out,
+                       int wave, int lane) const {
+    const int cg = lane & 15;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      Chunk<DT> c;
+      c.r[0] = r[i];
+      const float amax = group_max<16>(chunk_amax<DT>(c));
+      const Scales sc = block_scales(amax, a.fp8_max, a.eps);
+      const uint2 q = quant_chunk<DT, FMT>(c, sc.qs, a.fp8_max);
+      const int row = row_of(wave, lane, i);
+      *reinterpret_cast<uint2*>(tile + row * BK + (((cg >> 1) ^ swz(row)) << 4) + ((cg & 1) << 3)) = q;
+      if (cg == 0) sa[row] = sc.ds;
+      if (write_out && m0 + row < a.m) {
+        const int64_t mm = m0 + row;
+        *reinterpret_cast<uint2*>(a.qa_out + bidx * a.sqab + mm * a.sqam + int64_t(kb) * BK + cg * 8) = q;
+        if (cg == 0) a.sa_out[bidx * a.soab + mm * a.soam + int64_t(kb) * a.soak] = sc.ds;
+      }
+    }
+  }
+};
+
 template <int FMT>
 PCAMD_DEV v4f mfma(const v8i& x, const v8i& y, const v4f& c) {
   constexpr int code = FMT == kE5M2 ? 1 : 0;
@@ -185,10 +226,15 @@ __device__ __attribute__((noinline)) void epilogue_general(void* c, int64_t c_ro
 }
 
 // MODE: 0 block, 1 channel, 2 tensor. SB_COL: block mode with qbn < 16 (one
-// B scale per output column). QB1: block mode with qbk == 128.
-template <bool A_K, bool B_K, int FMT, int MODE, bool SB_COL, bool QB1>
+// B scale per output column). QB1: block mode with qbk == 128. ADT: -1 for an
+// fp8 A; kBF16 / kF16 for a 16-bit A quantized 1 x 128 in the kernel (block
+// mode, qbk == 128), its row scales kept in LDS behind the two stages.
+template <bool A_K, bool B_K, int FMT, int MODE, bool SB_COL, bool QB1, int ADT = -1>
 __global__ __launch_bounds__(NT, 1) void bmm_fast_kernel(FastArgs a) {
+  constexpr bool AQ = ADT == kBF16 || ADT == kF16;
+  static_assert(!AQ || (A_K && MODE == 0 && QB1), "fused A quantization: K-major A, 1 x 128 block scales");
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  float* sa_lds = reinterpret_cast<float*>(smem + 2 * STAGE);  // [2][BM], fused A quantization only
   const int t = threadIdx.x;
   const int lane = t & 63, wave = t >> 6;
   const int wm = wave & 1, wn = wave >> 1;
@@ -213,18 +259,23 @@ __global__ __launch_bounds__(NT, 1) void bmm_fast_kernel(FastArgs a) {
 
   MNStage<BM> ast;  // used when A is M-major
   MNStage<BN> bst;  // used when B is N-major
+  AQStage<AQ ? ADT : kBF16> aq;  // used when A is quantized here
+  const bool write_q = AQ && a.qa_out != nullptr && n0 == 0;
 
   auto issue = [&](int ks, uint8_t* stage) {
     const uint32_t k0 = ks * BK;
-    if constexpr (A_K) issue_kmajor<BM>(rsa, stage, m0, a.lda, k0, wave, lane);
+    if constexpr (A_K && !AQ) issue_kmajor<BM>(rsa, stage, m0, a.lda, k0, wave, lane);
     if constexpr (B_K) issue_kmajor<BN>(rsb, stage + A_BYTES, n0, a.ldb, k0, wave, lane);
   };
   auto load_mn = [&](int ks) {
     const uint32_t k0 = ks * BK;
+    if constexpr (AQ) aq.load(rsa, m0, a.lda, k0, wave, lane);
     if constexpr (!A_K) ast.load(rsa, m0, a.lda, k0, t);
     if constexpr (!B_K) bst.load(rsb, n0, a.ldb, k0, t);
   };
-  auto store_mn = [&](uint8_t* stage) {
+  // ks: the K step the stage is filled for
+  auto store_mn = [&](uint8_t* stage, int ks) {
+    if constexpr (AQ) aq.template store<FMT>(stage, sa_lds + (ks & 1) * BM, a, bidx, m0, ks, write_q, wave, lane);
     if constexpr (!A_K) ast.store(stage, t);
     if constexpr (!B_K) bst.store(stage + A_BYTES, t);
   };
@@ -250,7 +301,7 @@ __global__ __launch_bounds__(NT, 1) void bmm_fast_kernel(FastArgs a) {
   // prologue: stage 0
   load_mn(0);
   issue(0, smem);
-  store_mn(smem);
+  store_mn(smem, 0);
 
   for (int ks = 0; ks < ksteps; ++ks) {
     uint8_t* cur = smem + (ks & 1) * STAGE;
@@ -272,7 +323,8 @@ __global__ __launch_bounds__(NT, 1) void bmm_fast_kernel(FastArgs a) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int mm = row_base + 16 * i;
-          sav[i] = mm < a.m ? sab[int64_t(mm >> a.qbm_shift) * a.ssa1] : 0.0f;
+          if constexpr (AQ) sav[i] = sa_lds[(ks & 1) * BM + wm * 64 + 16 * i + lr];
+          else sav[i] = mm < a.m ? sab[int64_t(mm >> a.qbm_shift) * a.ssa1] : 0.0f;
         }
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
@@ -351,7 +403,7 @@ __global__ __launch_bounds__(NT, 1) void bmm_fast_kernel(FastArgs a) {
       }
     }
 
-    if (ks + 1 < ksteps) store_mn(nxt);
+    if (ks + 1 < ksteps) store_mn(nxt, ks + 1);
   }
 
   // ---- epilogue ----
@@ -595,7 +647,33 @@ int launch_layout(const FastArgs& a, bool a_k, bool b_k, int mode, bool sb_col, 
   return launch_mode<false, false, FMT>(a, mode, sb_col, qb1, st);
 }
 
+template <bool B_K, int FMT, bool SB_COL, int ADT>
+int launch_fused(const FastArgs& a, hipStream_t st) {
+  auto kern = bmm_fast_kernel<true, B_K, FMT, 0, SB_COL, true, ADT>;
+  constexpr int kLds = 2 * STAGE + 2 * BM * 4;  // two stages + the quantized A's row scales
+  static std::atomic<uint64_t> configured{0};   // devices whose LDS limit is set
+  const int rc = ensure_dynamic_lds(reinterpret_cast<const void*>(kern), kLds, st, configured);
+  if (rc != 0) return rc;
+  kern<<<a.total_tiles, NT, kLds, st>>>(a);
+  return check_launch("bmm_fast_kernel (fused A quantization)");
+}
+
+template <int FMT, int ADT>
+int launch_fused_layout(const FastArgs& a, bool b_k, bool sb_col, hipStream_t st) {
+  if (b_k) return sb_col ? launch_fused<true, FMT, true, ADT>(a, st) : launch_fused<true, FMT, false, ADT>(a, st);
+  return sb_col ? launch_fused<false, FMT, true, ADT>(a, st) : launch_fused<false, FMT, false, ADT>(a, st);
+}
+
 }  // namespace bmmf
+
+int bmm_fused_launch(const FastArgs& a, int a_dtype, int fmt, bool b_k, bool sb_col, hipStream_t st) {
+  if (fmt == kE5M2) {
+    if (a_dtype == kF16) return bmmf::launch_fused_layout<kE5M2, kF16>(a, b_k, sb_col, st);
+    return bmmf::launch_fused_layout<kE5M2, kBF16>(a, b_k, sb_col, st);
+  }
+  if (a_dtype == kF16) return bmmf::launch_fused_layout<kE4M3, kF16>(a, b_k, sb_col, st);
+  return bmmf::launch_fused_layout<kE4M3, kBF16>(a, b_k, sb_col, st);
+}
 
 int bmm_fast_launch(const FastArgs& a, int ab_dtype, bool a_k, bool b_k, int mode, bool sb_col, bool qb1,
                     hipStream_t st) {

@@ -201,6 +201,98 @@ def hip_per_block_bmm(
         _lib.SCALE_BLOCK, False, qbm, qbk, qbn, activation, batch, m, n, k)
 
 
+_UNSUPPORTED = -2  # PCAMD_ERR_UNSUPPORTED
+
+
+def hip_per_block_bmm_quant_a(
+    x: torch.Tensor,
+    b: QuantResult,
+    *,
+    eps: float = 1e-12,
+    out_dtype: torch.dtype = torch.bfloat16,
+    bias: Optional[torch.Tensor] = None,
+    out: Optional[torch.Tensor] = None,
+    activation: str = "none",
+    return_quant: bool = False,
+):
+    """``hip_per_block_bmm(hip_per_block_quant(x, block_m=1, block_n=128), b)``
+    with the activation quantization inside the GEMM's K loop.
+
+    x: bf16 or fp16 [B, M, K] (or [M, K] with a 3D b of batch 1), quantized in
+    1 x 128 groups along K into b's fp8 dtype; b: a block-scaled QuantResult
+    with quant-K block 128. The product equals the unfused path's bit for
+    bit: the A bytes and scales are those hip_per_block_quant produces. With
+    return_quant=True the quantized A comes back too, as (out, QuantResult).
+
+    This is the intent of the reference's fused quant + BMM kernel
+    (kernels/fp8_bmm/kernel/fp8_quant_bmm_fused_kernel.py:30-146, unfinished
+    there), on the per-block recipe. Layouts the fused kernel does not cover
+    (an M-major or unaligned x, K not a multiple of 128) take the two-kernel
+    path: hip_per_block_quant, then hip_per_block_bmm."""
+    if x.ndim not in (2, 3):
+        raise ValueError(f"fused quant BMM expects a 2D or 3D activation, got {tuple(x.shape)}")
+    if x.dtype not in (torch.bfloat16, torch.float16):
+        raise ValueError(f"fused quant BMM expects a bfloat16 or float16 activation, got {x.dtype}")
+    if activation not in ("none", "gelu"):
+        raise ValueError(f"activation must be 'none' or 'gelu', got {activation!r}")
+    x3 = x if x.ndim == 3 else x[None]
+    if b.tensor.ndim != 3:
+        raise ValueError("BMM expects a 3D quantized right operand")
+    b_qbk, qbn = _block_shape(b, "B")
+    if b_qbk != 128:
+        raise ValueError(f"the fused activation quantization uses quant-K blocks of 128; B has {b_qbk}")
+    fp8_dtype = b.tensor.dtype
+    in_b = C.matrix_layout(b.tensor, "B")
+    batch, m, k = x3.shape
+    b_batch, b_k, n = b.tensor.shape
+    if batch != b_batch or k != b_k:
+        raise ValueError(f"shape mismatch: A={tuple(x3.shape)}, B={tuple(b.tensor.shape)}")
+    if x3.device != b.tensor.device:
+        raise ValueError(f"A and B must be on the same device: A={x3.device}, B={b.tensor.device}")
+    _validate_scale(b, expected_shape=(batch, -(-k // 128), -(-n // qbn)), expected_block_m=128,
+                    expected_block_n=qbn, operand="B")
+    _lib.require_gpu_tensor(x3, "x")
+    out = C.prepare_out(out, out_dtype, batch, m, n, x3.device)
+    bias, bias_strides, bias_code = C.check_bias(bias, batch, m, n, x3.device)
+    qa = sa = None
+    if return_quant:
+        qa = torch.empty((batch, m, k), device=x3.device, dtype=fp8_dtype)
+        sa = torch.empty((batch, m, -(-k // 128)), device=x3.device, dtype=torch.float32)
+    L = _lib.lib()
+    rc = _UNSUPPORTED
+    if in_b in ("n-major", "k-major") and x3.stride(-1) == 1:
+        with torch.cuda.device(x3.device):
+            rc = L.pcamd_bmm_quant_a(
+                _lib.ptr(x3), _lib.dtype_code(x3.dtype), _lib.ptr(b.tensor), _lib.dtype_code(fp8_dtype),
+                batch, m, n, k, *x3.stride(), *b.tensor.stride(),
+                _lib.ptr(out), _lib.dtype_code(out.dtype), *out.stride(),
+                _lib.ptr(bias), bias_code, *bias_strides,
+                _lib.ptr(b.dequant_scale), *b.dequant_scale.stride(), qbn,
+                _lib.ptr(qa), *(qa.stride() if qa is not None else (0, 0, 0)),
+                _lib.ptr(sa), *(sa.stride() if sa is not None else (0, 0, 0)),
+                float(torch.finfo(fp8_dtype).max), float(eps),
+                _lib.ACT_GELU if activation == "gelu" else _lib.ACT_NONE, _lib.stream_of(x3))
+    if rc == _UNSUPPORTED:
+        qres = hip_per_block_quant(x3, block_m=1, block_n=128, fp8_dtype=fp8_dtype, eps=eps)
+        hip_per_block_bmm(qres, b, out_dtype=out_dtype, bias=bias, out=out, activation=activation)
+        if return_quant:
+            qa, sa = qres.tensor, qres.dequant_scale
+    else:
+        _lib.check(rc, "pcamd_bmm_quant_a")
+    if x.ndim == 2:
+        out = out.squeeze(0)
+    if not return_quant:
+        return out
+    quant = QuantResult(
+        tensor=qa if x.ndim == 3 else qa.squeeze(0),
+        dequant_scale=sa if x.ndim == 3 else sa.squeeze(0),
+        impl="hip_per_block",
+        granularity="block",
+        meta={"logical_shape": tuple(x.shape), "fp8_dtype": str(fp8_dtype), "block_m": 1, "block_n": 128},
+    )
+    return out, quant
+
+
 def _register_block_scheme(quant_impl: str, *, quant_block_m: int, quant_block_k: int,
                            quant_block_n: int, description: str) -> None:
     """Register the quantizer and its five BMM layout variants
