@@ -89,6 +89,14 @@ struct MNMajorLoader {
   PCAMD_DEV void issue(v4i rs, uint8_t* tile, uint32_t col0, uint32_t ld, uint32_t k0, int wave) const {
     issue(rs, lds_addr(tile), col0, ld, k0, wave);
   }
+  // instruction i of issue() alone (0 <= i < INSTS)
+  PCAMD_DEV void issue_one(v4i rs, uint32_t tile_lds, uint32_t col0, uint32_t ld, uint32_t k0, int wave,
+                           int i) const {
+    const int kb = wave * PER_WAVE + i * R;
+    uint32_t u = __builtin_amdgcn_readfirstlane((k0 + kb) * ld + col0);
+    asm volatile("" : "+s"(u));
+    lds_dma16(rs, tile_lds + kb * COLS, voff[i & 1] + u);
+  }
   // tile_lds: LDS byte address of the tile
   PCAMD_DEV void issue(v4i rs, uint32_t tile_lds, uint32_t col0, uint32_t ld, uint32_t k0, int wave) const {
 #pragma unroll

@@ -105,14 +105,15 @@ struct KMajorLoader {
 #pragma unroll
     for (int i = 0; i < INSTS; ++i) voff[i] = (row0 + wave * PER_WAVE + i * 8) * ld + lp;
   }
-  // tile_lds: LDS byte address of the tile
+  // instruction i (0 <= i < INSTS); tile_lds: LDS byte address of the tile
+  PCAMD_DEV void issue_one(v4i rs, uint32_t tile_lds, uint32_t k0, int wave, int i) const {
+    const uint32_t lds = tile_lds + (wave * PER_WAVE + i * 8) * BK;
+    asm volatile("buffer_load_dwordx4 %0, %1, %2 offen lds" ::"v"(voff[i]), "s"(rs), "s"(k0), "{m0}"(lds)
+                 : "memory");
+  }
   PCAMD_DEV void issue(v4i rs, uint32_t tile_lds, uint32_t k0, int wave) const {
 #pragma unroll
-    for (int i = 0; i < INSTS; ++i) {
-      const uint32_t lds = tile_lds + (wave * PER_WAVE + i * 8) * BK;
-      asm volatile("buffer_load_dwordx4 %0, %1, %2 offen lds" ::"v"(voff[i]), "s"(rs), "s"(k0), "{m0}"(lds)
-                   : "memory");
-    }
+    for (int i = 0; i < INSTS; ++i) issue_one(rs, tile_lds, k0, wave, i);
   }
 };
 
@@ -275,6 +276,18 @@ __global__ __launch_bounds__(NT, 1) void bmm_wide_kernel(FastArgs a) {
     if constexpr (B_K) load_b.issue(rsb, base + A_BYTES, k0, wave);
     else load_b.issue(rsb, base + A_BYTES, n0, a.ldb, k0, wave);
   };
+  // instruction q of the A / B loads of K step ks into `stage`
+  static_assert(LA::INSTS == 4 && LB::INSTS == 4, "DMA schedule assumes four load instructions per operand");
+  auto issue_a1 = [&](int ks, const uint8_t* stage, int q) {
+    const uint32_t k0 = __builtin_amdgcn_readfirstlane(ks * BK);
+    if constexpr (A_K) load_a.issue_one(rsa, lds_addr(stage), k0, wave, q);
+    else load_a.issue_one(rsa, lds_addr(stage), m0, a.lda, k0, wave, q);
+  };
+  auto issue_b1 = [&](int ks, const uint8_t* stage, int q) {
+    const uint32_t k0 = __builtin_amdgcn_readfirstlane(ks * BK);
+    if constexpr (B_K) load_b.issue_one(rsb, lds_addr(stage) + A_BYTES, k0, wave, q);
+    else load_b.issue_one(rsb, lds_addr(stage) + A_BYTES, n0, a.ldb, k0, wave, q);
+  };
   auto afrag = [&](const uint8_t* stage, int i) -> v8i {
     if constexpr (A_K) return frag_k(stage, wm * 64 + i * 16 + lr, lg);
     else return frag_mn<BM>(stage, wm * 64 + i * 16, lane);
@@ -305,12 +318,11 @@ __global__ __launch_bounds__(NT, 1) void bmm_wide_kernel(FastArgs a) {
     for (int j = 0; j < JN; ++j) acc[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
 
   const int ksteps = a.k / BK;  // >= 2
-  // prologue: step 0 resident in stage 0, step 1 in flight to stage 1
+  // prologue: step 0 resident in stage 0 (step 0's sub-tiles start step 1's DMA)
   issue(0, smem);
   if constexpr (MODE == 0) store_scale(0, load_scale(0));
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
-  issue(1, smem + STAGE);
   float sc_next = 0.0f;
   if constexpr (MODE == 0) sc_next = load_scale(1);
 
@@ -415,18 +427,36 @@ __global__ __launch_bounds__(NT, 1) void bmm_wide_kernel(FastArgs a) {
   };
 
   // One K step. BOUNDARY: the next step follows (barrier and fragment
-  // reads in front of sub-tile 7); DMA: also start the DMA two steps ahead.
-  // Both are compile-time so that the main loop body is one basic block:
-  // with a branch at the step boundary the compiler sinks the folds of the
-  // earlier sub-tiles past it and keeps all their partials live.
+  // reads in front of sub-tile 7); DMA: the step's first sub-tiles start the
+  // next step's global -> LDS loads; SCALES: fetch the block scales two steps
+  // ahead. All three are compile-time so that the main loop body is one basic
+  // block: with a branch at the step boundary the compiler sinks the folds of
+  // the earlier sub-tiles past it and keeps all their partials live.
+  //
+  // The next step's DMA goes to the other stage, which every wave has left
+  // at the previous boundary's barrier, and the boundary's vmcnt(0) + barrier
+  // publish it. Its eight load instructions are spread over the first
+  // sub-tiles (A in sub-tiles 0-1, B in 2-3 for whole tiles) rather than
+  // issued together at the boundary: the same loads in one burst right
+  // after the barrier made the forward GEMM of config 5 17 % slower.
+  constexpr int kSchedA[4] = {0, 0, 1, 1};
+  constexpr int kSchedB[4] = {JN == 8 ? 2 : 1, JN == 8 ? 2 : 1, JN == 8 ? 3 : 2, JN == 8 ? 3 : 2};
   constexpr int kBReads = B_K ? 2 : 4;  // ds_read instructions per B fragment
-  auto step = [&](int ks, auto boundary, auto dma) {
+  auto step = [&](int ks, auto boundary, auto dma, auto scales) {
     constexpr bool BOUNDARY = decltype(boundary)::value;
     constexpr bool DMA = decltype(dma)::value;
+    constexpr bool SCALES = decltype(scales)::value;
     const uint8_t* cur = smem + (ks & 1) * STAGE;
     const uint8_t* nxt = smem + ((ks + 1) & 1) * STAGE;
 #pragma unroll
     for (int j = 0; j < JN - 1; ++j) {
+      if constexpr (DMA) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          if (j == kSchedA[q]) issue_a1(ks + 1, nxt, q);
+          if (j == kSchedB[q]) issue_b1(ks + 1, nxt, q);
+        }
+      }
       const v8i bcur = bf[j & 1];
       bf[(j + 1) & 1] = bfrag(cur, j + 1);
       if constexpr (MODE == 0 && SBK != 0) read_cols(ks, j + 1);
@@ -436,10 +466,7 @@ __global__ __launch_bounds__(NT, 1) void bmm_wide_kernel(FastArgs a) {
       if constexpr (MODE == 0) store_scale(ks + 1, sc_next);
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
       __syncthreads();
-      if constexpr (DMA) {
-        issue(ks + 2, const_cast<uint8_t*>(cur));
-        if constexpr (MODE == 0) sc_next = load_scale(ks + 2);
-      }
+      if constexpr (MODE == 0 && SCALES) sc_next = load_scale(ks + 2);
       bf[0] = bfrag(nxt, 0);
       if constexpr (MODE == 0) {
         // cs[1] (sub-tile 7) is still needed; cs[0] takes sub-tile 0 of the next step
@@ -459,9 +486,9 @@ __global__ __launch_bounds__(NT, 1) void bmm_wide_kernel(FastArgs a) {
       subtile(JN - 1, bf[1], nullptr, IC<0>{}, F{});
     }
   };
-  for (int ks = 0; ks < ksteps - 2; ++ks) step(ks, T{}, T{});
-  step(ksteps - 2, T{}, F{});
-  step(ksteps - 1, F{}, F{});
+  for (int ks = 0; ks < ksteps - 2; ++ks) step(ks, T{}, T{}, T{});
+  step(ksteps - 2, T{}, T{}, F{});
+  step(ksteps - 1, F{}, F{}, F{});
   if constexpr (MODE == 0) {
 #pragma unroll
     for (int i = 0; i < 4; ++i)
