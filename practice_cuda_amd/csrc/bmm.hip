@@ -491,12 +491,17 @@ extern "C" int pcamd_bmm_scaled(const void* a, const void* b, int ab_dtype, int6
 
   // tuned path: K a multiple of 128, 16-byte aligned operands and rows,
   // power-of-two block sizes, 32-bit addressable batch slices.
-  // PCAMD_BMM_WIDE=0 / PCAMD_BMM_GENERIC select the other kernels (read once)
+  // PCAMD_BMM_WIDE=0 / PCAMD_BMM_STREAM=0 / PCAMD_BMM_GENERIC select the other
+  // kernels (read once)
   static const bool env_no_wide = [] {
     const char* e = getenv("PCAMD_BMM_WIDE");
     return e && e[0] == '0';
   }();
   static const bool env_generic = getenv("PCAMD_BMM_GENERIC") != nullptr;
+  static const bool env_no_stream = [] {
+    const char* e = getenv("PCAMD_BMM_STREAM");
+    return e && e[0] == '0';
+  }();
   {
     const bool wide = k >= 256 && (scale_mode != PCAMD_SCALE_BLOCK || args.qbk == 128) && !env_no_wide;
     const int64_t TM = wide ? bmm_wide_tile() : bmm_fast_tile_m();
@@ -531,6 +536,8 @@ extern "C" int pcamd_bmm_scaled(const void* a, const void* b, int ab_dtype, int6
       const int fmode = scale_mode == PCAMD_SCALE_BLOCK ? 0 : scale_mode == PCAMD_SCALE_CHANNEL ? 1 : 2;
       const bool sb_col = scale_mode == PCAMD_SCALE_BLOCK && args.qbn < 16;
       const bool qb1 = scale_mode == PCAMD_SCALE_BLOCK && args.qbk == 128;
+      if (!env_no_stream && bmm_stream_ok(f, a_k, b_k, fmode, batch, args.qbm, args.qbn, ssa1, ssb2))
+        return bmm_stream_launch(f, ab_dtype, batch, st);
       if (wide) return bmm_wide_launch(f, ab_dtype, a_k, b_k, fmode, st);
       return bmm_fast_launch(f, ab_dtype, a_k, b_k, fmode, sb_col, qb1, st);
     }

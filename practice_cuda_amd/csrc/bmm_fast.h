@@ -50,6 +50,13 @@ int bmm_fast_tile_n();
 // of B and of the quantized A
 int bmm_fused_launch(const FastArgs& a, int a_dtype, int fmt, bool b_k, bool sb_col, hipStream_t st);
 
+// persistent streaming kernel for K == 128, N == 512, A K-major, B N-major,
+// 1 x 128 A scales and column-block B scales, plain bf16 output
+// (bmm_stream.hip); bmm_stream_ok is the host-side envelope check
+bool bmm_stream_ok(const FastArgs& a, bool a_k, bool b_k, int mode, int64_t batch, int64_t qbm, int64_t qbn,
+                   int64_t ssa1, int64_t ssb2);
+int bmm_stream_launch(const FastArgs& a, int ab_dtype, int64_t batch, hipStream_t st);
+
 // 256 x 256-tile, 8-wave kernel for two or more K steps (bmm_wide.hip)
 // block mode requires quant_block_k == 128 and power-of-two qbm / qbn
 int bmm_wide_launch(const FastArgs& a, int ab_dtype, bool a_k, bool b_k, int mode, hipStream_t st);
