@@ -35,6 +35,29 @@ HBM_PEAK_GBS = 8000.0        # MI355X HBM3E
 HEADLINE_KERNEL = "quant_rowblock_kernel<bf16,e4m3,4,nt,grid2> (256 threads)"
 FP8_PEAK_TFLOPS = 5000.0     # MI355X dense fp8 MFMA (5.0 PFLOP/s)
 SETTLE_MS = 100.0            # untimed load before the first (headline) measurement
+# the kernels configs 4 and 5 launch (as rocprofv3 names them), to match the
+# committed counter summary (profiles/pmc_bmm.json) to the code that runs now
+CONFIG4_KERNEL = "pcamd::bmms::bmm_stream_kernel<3>"
+CONFIG5_KERNELS = {"fwd_a_k_b_k": ("fwd", ["pcamd::bmmw::bmm_wide_kernel<true, true, 3, 0, 0, 8>"]),
+                   "dgrad_a_k_b_n": ("dgrad", ["pcamd::bmmw::bmm_wide_kernel<true, false, 3, 0, 0, 8>"]),
+                   "wgrad_a_m_b_n": ("wgrad_a_m_b_n", ["pcamd::bmmw::bmm_wide_kernel<false, false, 3, 0, 2, 4>",
+                                                       "pcamd::bmmw::bmm_wide_kernel<false, false, 3, 0, 2, 8>"])}
+
+
+def pmc_field(workload, kernels, keys):
+    """Sum of `keys` of one workload in profiles/pmc_bmm.json (rocprofv3
+    counter passes), or None when that file is missing or was taken on
+    other kernels than `kernels` (a str or a list of names)."""
+    path = os.path.join(ROOT, "profiles", "pmc_bmm.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as fh:
+        rec = json.load(fh).get("workloads", {}).get(workload)
+    want = sorted([kernels] if isinstance(kernels, str) else kernels)
+    if not rec or sorted(rec.get("kernels", [])) != want:
+        return None
+    vals = [rec.get(k) for k in (keys if isinstance(keys, tuple) else (keys,))]
+    return None if any(v is None for v in vals) else sum(vals)
 
 
 def parse():
@@ -45,6 +68,9 @@ def parse():
     p.add_argument("--no-components", action="store_true")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--components-only", default="", help="comma list of component names")
+    p.add_argument("--pmc-probe-bmm", action="store_true",
+                   help="eager launches for rocprofv3 --pmc passes: 3 plain bf16 copies of 256 MiB, then 3 "
+                        "each of config 4 and the config-5 forward, dgrad, wgrad and layer wgrad")
     p.add_argument("--pmc-probe", action="store_true",
                    help="eager launches for rocprofv3 --pmc passes: 3 plain bf16 copies of "
                         "256 MiB (calibration) then 3 config-2 quantizations")
@@ -229,7 +255,9 @@ def bench_quant(torch, name, x_cpu, kind, steps, warmup, nsets, dev, bm=1, bn=12
 # ---------------------------------------------------------------------------
 # BMM workloads
 # ---------------------------------------------------------------------------
-def bench_config4(torch, steps, warmup, dev, nsets=4):
+def config4_launcher(torch, dev, nsets):
+    """BASELINE config 4 over nsets rotating operand / output sets: launch(i)
+    runs the block-scaled BMM on set i % nsets through the C ABI."""
     from practice_cuda_amd import _lib as L
     from practice_cuda_amd.impls.hip_per_block import hip_per_block_quant
     g = torch.Generator().manual_seed(0)
@@ -252,6 +280,11 @@ def bench_config4(torch, steps, warmup, dev, nsets=4):
             L.SCALE_BLOCK, 0, 1, 128, 128, L.ACT_NONE, L.stream_of(c))
         L.check(rc, "pcamd_bmm_scaled")
 
+    return launch
+
+
+def bench_config4(torch, steps, warmup, dev, nsets=4):
+    launch = config4_launcher(torch, dev, nsets)
     # ~100 ms of untimed launches first: the clocks settle under this load
     # (without it the five replays of a cold start fall from ~58 to ~50 us)
     ms, samples = graph_time(torch, launch, steps, warmup, settle_ms=SETTLE_MS)
@@ -264,32 +297,46 @@ def bench_config4(torch, steps, warmup, dev, nsets=4):
             "value": tflops, "unit": "TFLOP/s", "frac_of_fp8_peak": tflops / FP8_PEAK_TFLOPS,
             "hbm_GBps": gbs, "frac_of_hbm_peak": gbs / HBM_PEAK_GBS,
             "frac_of_attainable_roofline": tflops / attainable, "bytes_per_step": nbytes,
-            "flops_per_step": flops}
+            "flops_per_step": flops,
+            "roofline": {"bound": "hbm", "achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": gbs / HBM_PEAK_GBS, "kernel": CONFIG4_KERNEL,
+                         "traffic": pmc_field("config4", CONFIG4_KERNEL, ("fetch_bytes", "write_bytes"))}}
 
 
-def bench_config5(torch, steps, warmup, dev):
-    """FP8 training-linear GEMM trio at M=8192 K=4096 N=14336: fwd X W^T
-    (a_k_b_k), dgrad dY W (a_k_b_n), wgrad dY^T X (a_m_b_n, 128x1 requant)."""
-    from practice_cuda_amd.impls.hip_per_block import hip_per_block_bmm, hip_per_block_quant
+def config5_operands(torch, dev):
+    """BASELINE config 5 (M=8192 K=4096 N=14336), CPU generator seed 0:
+    the bf16 tensors and their block quantizations."""
+    from practice_cuda_amd.impls.hip_per_block import hip_per_block_quant
     M, K, N = 8192, 4096, 14336
     g = torch.Generator().manual_seed(0)
     X = torch.randn(M, K, generator=g).bfloat16().to(dev)
     W = (torch.randn(N, K, generator=g) * 0.02).bfloat16().to(dev)
     dY = (torch.randn(M, N, generator=g) * 1e-3).bfloat16().to(dev)
-    qx = hip_per_block_quant(X[None], block_m=1, block_n=128)            # [1, M, K] 1x128
-    qw = hip_per_block_quant(W[None], block_m=128, block_n=128)          # [1, N, K] 128x128
-    qdy = hip_per_block_quant(dY[None], block_m=1, block_n=128)          # [1, M, N] 1x128
-    qdy_m = hip_per_block_quant(dY[None], block_m=128, block_n=1)        # [1, M, N] 128x1
-    qx_m = hip_per_block_quant(X[None], block_m=128, block_n=1)          # [1, M, K] 128x1
-    from practice_cuda_amd.registry import QuantResult
+    q = {
+        "x": hip_per_block_quant(X[None], block_m=1, block_n=128),      # [1, M, K] 1x128
+        "w": hip_per_block_quant(W[None], block_m=128, block_n=128),    # [1, N, K] 128x128
+        "dy": hip_per_block_quant(dY[None], block_m=1, block_n=128),    # [1, M, N] 1x128
+        "dy_m": hip_per_block_quant(dY[None], block_m=128, block_n=1),  # [1, M, N] 128x1
+        "x_m": hip_per_block_quant(X[None], block_m=128, block_n=1),    # [1, M, K] 128x1
+    }
+    return (M, K, N), (X, W, dY), q
 
-    def tr(q: QuantResult, bm, bn):
+
+def config5_gemms(torch, dev, q, dims):
+    """The trio (fwd X W^T a_k_b_k, dgrad dY W a_k_b_n, wgrad dY^T X a_m_b_n
+    with the 128x1 requant) as launch closures over preallocated outputs."""
+    from practice_cuda_amd.impls.hip_per_block import hip_per_block_bmm
+    from practice_cuda_amd.registry import QuantResult
+    M, K, N = dims
+
+    def tr(r: QuantResult, bm, bn):
         # logical transpose of the last two dims (a strided view) with its scales
-        return QuantResult(q.tensor.transpose(-1, -2), q.dequant_scale.transpose(-1, -2), q.impl,
+        return QuantResult(r.tensor.transpose(-1, -2), r.dequant_scale.transpose(-1, -2), r.impl,
                            "block", {"block_m": bn, "block_n": bm})
 
+    qx, qw, qdy, qx_m = q["x"], q["w"], q["dy"], q["x_m"]
     wt = tr(qw, 128, 128)         # B = W^T  [1, K, N], K-major     (fwd)
-    dyt = tr(qdy_m, 128, 1)       # A = dY^T [1, N, M], M-major     (wgrad), 1x128 over M
+    dyt = tr(q["dy_m"], 128, 1)   # A = dY^T [1, N, M], M-major     (wgrad), 1x128 over M
     out_f = torch.empty(1, M, N, dtype=torch.bfloat16, device=dev)
     out_d = torch.empty(1, M, K, dtype=torch.bfloat16, device=dev)
     out_w = torch.empty(1, N, K, dtype=torch.bfloat16, device=dev)
@@ -298,6 +345,18 @@ def bench_config5(torch, steps, warmup, dev):
         "dgrad_a_k_b_n": lambda i: hip_per_block_bmm(qdy, qw, out=out_d),
         "wgrad_a_m_b_n": lambda i: hip_per_block_bmm(dyt, qx_m, out=out_w),
     }
+    return gemms, dyt, (out_f, out_d, out_w)
+
+
+def bench_config5(torch, steps, warmup, dev):
+    """FP8 training-linear GEMM trio at M=8192 K=4096 N=14336: fwd X W^T
+    (a_k_b_k), dgrad dY W (a_k_b_n), wgrad dY^T X (a_m_b_n, 128x1 requant)."""
+    from practice_cuda_amd.impls.hip_per_block import hip_per_block_bmm
+    from practice_cuda_amd.registry import QuantResult
+    dims, (X, W, dY), q = config5_operands(torch, dev)
+    M, K, N = dims
+    qx, qw, qdy, qdy_m, qx_m = q["x"], q["w"], q["dy"], q["dy_m"], q["x_m"]
+    gemms, dyt, (out_f, out_d, out_w) = config5_gemms(torch, dev, q, dims)
     flops = 2 * M * N * K
     res = {}
     for name, fn in gemms.items():
@@ -327,7 +386,7 @@ def bench_config5(torch, steps, warmup, dev):
                                   "note": "channel scales (per-channel recipe); not in the trio total"}
     del cx, cw, cwt
     tflops = 3 * flops / (total_ms * 1e-3) / 1e12
-    del qx, qw, qdy, qdy_m, qx_m, wt, dyt, out_f, out_d, out_w, gemms
+    del qx, qw, qdy, qdy_m, qx_m, dyt, out_f, out_d, out_w, gemms, q
     torch.cuda.empty_cache()
     # the layer step's quantization launches: X and dY each quantized 1x128
     # and 128x1 by one kernel, W 128x128
@@ -338,9 +397,16 @@ def bench_config5(torch, steps, warmup, dev):
         q.pop("samples_ms", None)
     layer = layer_step(torch, X, W, dY, steps, dev)
     layer["TFLOP/s"] = 3 * flops / (layer["ms"] * 1e-3) / 1e12
+    # roofline of the trio: MFMA-bound; busy fractions from the committed
+    # counter passes when they were taken on the kernels that run now
+    busy = {name: pmc_field(wl, ks, "mfma_busy") for name, (wl, ks) in CONFIG5_KERNELS.items()}
+    roof = {"bound": "mfma", "achieved": tflops, "peak": FP8_PEAK_TFLOPS, "unit": "TFLOP/s",
+            "frac": tflops / FP8_PEAK_TFLOPS, "flops_per_gemm": flops,
+            "kernels": {name: ks for name, (_, ks) in CONFIG5_KERNELS.items()},
+            "mfma_busy": busy if all(v is not None for v in busy.values()) else None}
     return {"name": "config5_training_linear_m8192_k4096_n14336", "ms_per_step": total_ms,
             "value": tflops, "unit": "TFLOP/s", "frac_of_fp8_peak": tflops / FP8_PEAK_TFLOPS,
-            "gemms": res, "flops_per_step": 3 * flops, "quant": quants, "layer_step": layer}
+            "gemms": res, "flops_per_step": 3 * flops, "roofline": roof, "quant": quants, "layer_step": layer}
 
 
 def layer_step(torch, X, W, dY, steps, dev):
@@ -598,6 +664,41 @@ def pmc_probe(torch, dev):
                       "quant_bytes_read": x2.numel() * 2, "quant_bytes_written": x2.numel() + x2.shape[0] * 4}))
 
 
+def pmc_probe_bmm(torch, dev):
+    """Eager launches for rocprofv3 --pmc passes over the BMM kernels, each
+    dispatch carrying its own counters: three 256 MiB bf16 copies
+    (calibration), then three launches each of config 4 and of the config-5
+    forward, dgrad, wgrad (a_m_b_n) and the layer's K-major wgrad, in that
+    order."""
+    from practice_cuda_amd.impls.hip_per_block import hip_per_block_bmm
+    from practice_cuda_amd.registry import QuantResult
+    src = torch.ones(1 << 27, dtype=torch.bfloat16, device=dev)  # 256 MiB
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    del src, dst
+    launch4 = config4_launcher(torch, dev, 3)
+    for i in range(3):
+        launch4(i)
+    torch.cuda.synchronize()
+    del launch4
+    torch.cuda.empty_cache()
+    dims, _, q = config5_operands(torch, dev)
+    gemms, dyt, outs = config5_gemms(torch, dev, q, dims)
+    dyt_k = QuantResult(dyt.tensor.contiguous(), dyt.dequant_scale, dyt.impl, "block", dict(dyt.meta))
+    qx_m = q["x_m"]
+    qx_mk = QuantResult(qx_m.tensor.transpose(-1, -2).contiguous().transpose(-1, -2), qx_m.dequant_scale,
+                        qx_m.impl, "block", dict(qx_m.meta))
+    gemms["wgrad_layer_a_k_b_k"] = lambda i: hip_per_block_bmm(dyt_k, qx_mk, out=outs[2])
+    for name, fn in gemms.items():
+        for i in range(3):
+            fn(i)
+        torch.cuda.synchronize()
+    print(json.dumps({"copy_bytes_read": (1 << 28), "copy_bytes_written": (1 << 28),
+                      "order": ["copy x3", "config4 x3"] + [f"{k} x3" for k in gemms]}))
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -613,6 +714,9 @@ def main():
 
     if args.pmc_probe:
         pmc_probe(torch, dev)
+        return
+    if args.pmc_probe_bmm:
+        pmc_probe_bmm(torch, dev)
         return
 
     x2 = make_config2(torch)
