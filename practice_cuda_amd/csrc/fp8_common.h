@@ -9,6 +9,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 #include "../../include/pcamd_fp8.h"
 
 #define PCAMD_DEV __device__ __forceinline__
@@ -107,6 +109,21 @@ PCAMD_DEV float chunk_amax(const Chunk<DT>& c) {
   return fmaxf(fmaxf(a, b), fmaxf(d, e));
 }
 
+// bf16 pairs as raw bits: |x| clears the sign bits, and non-negative bf16
+// values order like their bit patterns, so the max of |x| over a chunk is an
+// unsigned 16-bit max (v_pk_max_u16 does two per instruction). NaN inputs are
+// outside the quantizers' contract.
+typedef unsigned short u16x2_t __attribute__((ext_vector_type(2)));
+PCAMD_DEV uint32_t bf16_abs2(uint32_t w) { return w & 0x7FFF7FFFu; }
+PCAMD_DEV uint32_t pk_max_u16(uint32_t a, uint32_t b) {
+  return __builtin_bit_cast(uint32_t,
+                            __builtin_elementwise_max(__builtin_bit_cast(u16x2_t, a), __builtin_bit_cast(u16x2_t, b)));
+}
+// the larger of the two 16-bit halves, zero-extended
+PCAMD_DEV uint32_t max_halves(uint32_t m) { return max(m & 0xFFFFu, m >> 16); }
+// bf16 bit pattern (low 16 bits) -> float
+PCAMD_DEV float bf16_bits(uint32_t b) { return __uint_as_float(b << 16); }
+
 // ---------------------------------------------------------------------------
 // wavefront reductions: max over aligned groups of LANES lanes (power of 2)
 // ---------------------------------------------------------------------------
@@ -135,6 +152,28 @@ PCAMD_DEV float group_max(float v) {
   }
   if constexpr (LANES >= 64) v = fmaxf(v, __shfl_xor(v, 32, 64));
   return v;
+}
+
+// Unsigned max over aligned groups of LANES (<= 16) lanes. 0 is the identity
+// of the max, so each step can fold its DPP move into the max.
+template <int LANES>
+PCAMD_DEV uint32_t group_max_u32(uint32_t v) {
+  static_assert(LANES <= 16, "row-local DPP steps only");
+  auto step = [](uint32_t x, auto ctrl) {
+    return max(x, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(x), decltype(ctrl)::value,
+                                                                     0xF, 0xF, false)));
+  };
+  if constexpr (LANES >= 2) v = step(v, std::integral_constant<int, kDppQuadXor1>{});
+  if constexpr (LANES >= 4) v = step(v, std::integral_constant<int, kDppQuadXor2>{});
+  if constexpr (LANES >= 8) v = step(v, std::integral_constant<int, kDppRowHalfMirror>{});
+  if constexpr (LANES >= 16) v = step(v, std::integral_constant<int, kDppRowMirror>{});
+  return v;
+}
+
+// value of lane P of this lane's quad (DPP quad_perm [P, P, P, P])
+template <int P>
+PCAMD_DEV float quad_bcast(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), P * 0x55, 0xF, 0xF, false));
 }
 
 // ---------------------------------------------------------------------------
@@ -195,6 +234,28 @@ PCAMD_DEV uint2 quant_chunk(const Chunk<DT>& c, float qs, float fp8_max) {
 #pragma unroll
   for (int i = 0; i < 8; ++i) v[i] = clamp_sym(v[i] * qs, fp8_max);
   return make_uint2(pack4<FMT>(v[0], v[1], v[2], v[3]), pack4<FMT>(v[4], v[5], v[6], v[7]));
+}
+
+// Largest finite value of the format.
+template <int FMT>
+constexpr float fmt_max() {
+  return FMT == kE5M2 ? 57344.0f : 448.0f;
+}
+
+// Quantize 8 fp32 values (x * qs, clamped to +-fp8_max when CLAMP). The
+// clamp of the reference (tl.clamp before the cast) can be left out when
+// fp8_max is the format's largest finite value and qs = fp8_max / s with s at
+// least the max |x| of the values it scales: then |fl(x * qs)| <= fp8_max *
+// (1 + 2^-23), below the rounding midpoint to the next (non-finite) code
+// (464 for e4m3fn, 59392 for e5m2), and round-to-nearest-even gives the
+// clamped value's code. The conversion self-test pins the hardware converter
+// up to those midpoints.
+template <int FMT, bool CLAMP>
+PCAMD_DEV uint2 quant8(const float (&v)[8], float qs, float fp8_max) {
+  float q[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) q[i] = CLAMP ? clamp_sym(v[i] * qs, fp8_max) : v[i] * qs;
+  return make_uint2(pack4<FMT>(q[0], q[1], q[2], q[3]), pack4<FMT>(q[4], q[5], q[6], q[7]));
 }
 
 template <int DT, int FMT>

@@ -609,7 +609,8 @@ __global__ void tensor_finalize_kernel(TensorArgs a) {
 // ===========================================================================
 template <int FMT>
 __global__ __launch_bounds__(kThreads) void selftest_convert_kernel(uint32_t* result, uint32_t limit) {
-  // Every pattern p in [0, limit] (limit = bits of the fp8 max) is converted
+  // Every pattern p in [0, limit] (limit: bits of the rounding midpoint above
+  // the fp8 max) is converted
   // in lane position 0 of a packed quadruple (x, y, -x, w) with y and w drawn
   // from other patterns of the range, so sign handling and the byte order of
   // the packed result are checked along with the rounding.
@@ -869,17 +870,26 @@ PCAMD_DEV void byte_transpose4(uint32_t d0, uint32_t d1, uint32_t d2, uint32_t d
 // TCOL: the 128 x 1 output is stored transposed (element (r, c) at
 // c * ycn + r): each lane turns its 4 rows x 8 columns of fp8 bytes into 8
 // words of 4 rows (byte transposes), the block passes through 16 KiB of LDS,
-// and the transposed rows leave as 16-byte stores. Needs whole blocks. Each row's 128 columns sit in one aligned 16-lane
-// row of the wave (DPP max); column maxima meet as in quant_colgroup_kernel
-// (lane shuffles, then LDS across the waves). The results are those of the
-// 1 x 128 and 128 x 1 quantizers run separately. FULL: m and n are multiples
-// of 128, so no bounds checks.
-template <int DT, int FMT, int NT, bool NTS, bool FULL, bool TCOL>
+// and the transposed rows leave as 16-byte stores. Needs whole blocks. Each
+// row's 128 columns sit in one aligned 16-lane row of the wave (DPP max);
+// column maxima meet through lane shuffles, then LDS across the waves. The
+// results are those of the 1 x 128 and 128 x 1 quantizers run separately.
+// FULL: m and n are multiples of 128, so no bounds checks. CLAMP: clamp
+// x * qs to +-fp8_max before the cast (needed only when fp8_max is not the
+// format's largest finite value, see quant8).
+//
+// bf16 input with four rows per lane (PK) works on the raw bits: |x| maxima
+// are packed unsigned 16-bit maxima (two per instruction), and of the four
+// row groups a 16-lane row slice holds, lane (t % 16) forms the scales of
+// group (t % 4) only - one division pair per lane instead of four - which
+// its quad then broadcasts back. Same bits as the float path.
+template <int DT, int FMT, int NT, bool NTS, bool FULL, bool TCOL, bool CLAMP>
 __global__ __launch_bounds__(NT) void quant_dual_kernel(DualArgs a) {
   constexpr int EB = elem_bytes<DT>();
   constexpr int CPT = 2048 / NT, WAVES = NT / 64, RPP = NT / 16;
+  constexpr bool PK = DT == kBF16 && CPT == 4;
   static_assert(!TCOL || (FULL && CPT == 4), "transposed column output: whole blocks, four rows per lane");
-  __shared__ float part[WAVES][128];
+  __shared__ float part[WAVES][128];  // PK: [WAVES][64] packed column-pair maxima
   __shared__ float qsv[128];
   // transposed block: 128 columns x 32 words of 4 rows; the 16-byte groups of
   // column c sit XOR-ed with (c / 8) % 8 so that the word writes are at most
@@ -890,46 +900,93 @@ __global__ __launch_bounds__(NT) void quant_dual_kernel(DualArgs a) {
   const int64_t b = blockIdx.z, g = blockIdx.y, strip = blockIdx.x;
   const int64_t col = strip * 128 + lc * 8;
   const int64_t r0 = g * 128;
+  auto row_of = [&](int p) -> int64_t { return TCOL ? r0 + 4 * rs + p : r0 + p * RPP + rs; };
   const char* xb = a.x + b * a.sxb * EB;
   Chunk<DT> raw[CPT];
 #pragma unroll
   for (int p = 0; p < CPT; ++p) {
-    const int64_t r = TCOL ? r0 + 4 * rs + p : r0 + p * RPP + rs;
+    const int64_t r = row_of(p);
     if (FULL || (r < a.m && col < a.n)) load_chunk<DT>(raw[p], xb + (r * a.sxm + col) * EB);
     else zero_chunk<DT>(raw[p]);
   }
-  // 1 x 128: one group per row of the strip
   float rq[CPT];
+  uint32_t* partu = reinterpret_cast<uint32_t*>(&part[0][0]);
+  if constexpr (PK) {
+    uint32_t ab[CPT][4];
 #pragma unroll
-  for (int p = 0; p < CPT; ++p) {
-    const Scales s = block_scales(group_max<16>(chunk_amax<DT>(raw[p])), a.fp8_max, a.eps);
-    rq[p] = s.qs;
-    const int64_t r = TCOL ? r0 + 4 * rs + p : r0 + p * RPP + rs;
-    if (lc == 0 && (FULL || r < a.m)) a.sr[b * a.srb + r * a.srm + strip * a.srn] = s.ds;
-  }
-  // 128 x 1: one group per column of the strip
-  float cmax[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    for (int p = 0; p < CPT; ++p) {
+      ab[p][0] = bf16_abs2(raw[p].r[0].x); ab[p][1] = bf16_abs2(raw[p].r[0].y);
+      ab[p][2] = bf16_abs2(raw[p].r[0].z); ab[p][3] = bf16_abs2(raw[p].r[0].w);
+    }
+    // 1 x 128: one group per row of the strip
+    uint32_t rm[CPT];
 #pragma unroll
-  for (int p = 0; p < CPT; ++p) {
-    float v[8];
-    unpack_chunk<DT>(raw[p], v);
+    for (int p = 0; p < CPT; ++p)
+      rm[p] = group_max_u32<16>(max_halves(pk_max_u16(pk_max_u16(ab[p][0], ab[p][1]), pk_max_u16(ab[p][2], ab[p][3]))));
+    const int sel = lc & 3;
+    const uint32_t ms = sel == 0 ? rm[0] : sel == 1 ? rm[1] : sel == 2 ? rm[2] : rm[3];
+    const Scales s = block_scales(bf16_bits(ms), a.fp8_max, a.eps);
+    rq[0] = quad_bcast<0>(s.qs); rq[1] = quad_bcast<1>(s.qs);
+    rq[2] = quad_bcast<2>(s.qs); rq[3] = quad_bcast<3>(s.qs);
+    if (lc < CPT) {
+      const int64_t r = row_of(lc);
+      if (FULL || r < a.m) a.sr[b * a.srb + r * a.srm + strip * a.srn] = s.ds;
+    }
+    // 128 x 1: column-pair maxima over this lane's rows, the 4 row slices of
+    // the wave (lane shuffles), then the waves (LDS)
+    uint32_t cm[4];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) cmax[i] = fmaxf(cmax[i], fabsf(v[i]));
-  }
+    for (int w = 0; w < 4; ++w) {
+      cm[w] = pk_max_u16(pk_max_u16(ab[0][w], ab[1][w]), pk_max_u16(ab[2][w], ab[3][w]));
+      cm[w] = pk_max_u16(cm[w], static_cast<uint32_t>(__shfl_xor(static_cast<int>(cm[w]), 16)));
+      cm[w] = pk_max_u16(cm[w], static_cast<uint32_t>(__shfl_xor(static_cast<int>(cm[w]), 32)));
+    }
+    if ((t & 63) < 16) {
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    cmax[i] = fmaxf(cmax[i], __shfl_xor(cmax[i], 16));
-    cmax[i] = fmaxf(cmax[i], __shfl_xor(cmax[i], 32));
-  }
-  if ((t & 63) < 16) {
+      for (int w = 0; w < 4; ++w) partu[(t >> 6) * 64 + lc * 4 + w] = cm[w];
+    }
+  } else {
+    // 1 x 128: one group per row of the strip
 #pragma unroll
-    for (int i = 0; i < 8; ++i) part[t >> 6][lc * 8 + i] = cmax[i];
+    for (int p = 0; p < CPT; ++p) {
+      const Scales s = block_scales(group_max<16>(chunk_amax<DT>(raw[p])), a.fp8_max, a.eps);
+      rq[p] = s.qs;
+      const int64_t r = row_of(p);
+      if (lc == 0 && (FULL || r < a.m)) a.sr[b * a.srb + r * a.srm + strip * a.srn] = s.ds;
+    }
+    // 128 x 1: one group per column of the strip
+    float cmax[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+    for (int p = 0; p < CPT; ++p) {
+      float v[8];
+      unpack_chunk<DT>(raw[p], v);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) cmax[i] = fmaxf(cmax[i], fabsf(v[i]));
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      cmax[i] = fmaxf(cmax[i], __shfl_xor(cmax[i], 16));
+      cmax[i] = fmaxf(cmax[i], __shfl_xor(cmax[i], 32));
+    }
+    if ((t & 63) < 16) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) part[t >> 6][lc * 8 + i] = cmax[i];
+    }
   }
   __syncthreads();
   if (t < 128) {
-    float mx = part[0][t];
+    float mx;
+    if constexpr (PK) {
+      // column t: dword t / 2 of each wave's row, its low half for even t
+      uint32_t m = 0;
 #pragma unroll
-    for (int w = 1; w < WAVES; ++w) mx = fmaxf(mx, part[w][t]);
+      for (int w = 0; w < WAVES; ++w) m = max(m, (partu[w * 64 + (t >> 1)] >> ((t & 1) * 16)) & 0xFFFFu);
+      mx = bf16_bits(m);
+    } else {
+      mx = part[0][t];
+#pragma unroll
+      for (int w = 1; w < WAVES; ++w) mx = fmaxf(mx, part[w][t]);
+    }
     const Scales sc = block_scales(mx, a.fp8_max, a.eps);
     qsv[t] = sc.qs;
     const int64_t c = strip * 128 + t;
@@ -943,14 +1000,15 @@ __global__ __launch_bounds__(NT) void quant_dual_kernel(DualArgs a) {
   uint2 qcol[CPT];
 #pragma unroll
   for (int p = 0; p < CPT; ++p) {
-    const int64_t r = TCOL ? r0 + 4 * rs + p : r0 + p * RPP + rs;
+    const int64_t r = row_of(p);
     if (FULL || (r < a.m && col < a.n)) {
-      store8<DT, NTS>(yrb + r * a.sym + col, quant_chunk<DT, FMT>(raw[p], rq[p], a.fp8_max));
       float v[8];
       unpack_chunk<DT>(raw[p], v);
+      store8<DT, NTS>(yrb + r * a.sym + col, quant8<FMT, CLAMP>(v, rq[p], a.fp8_max));
+      float w[8];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) v[i] = clamp_sym(v[i] * qc[i], a.fp8_max);
-      qcol[p] = make_uint2(pack4<FMT>(v[0], v[1], v[2], v[3]), pack4<FMT>(v[4], v[5], v[6], v[7]));
+      for (int i = 0; i < 8; ++i) w[i] = CLAMP ? clamp_sym(v[i] * qc[i], a.fp8_max) : v[i] * qc[i];
+      qcol[p] = make_uint2(pack4<FMT>(w[0], w[1], w[2], w[3]), pack4<FMT>(w[4], w[5], w[6], w[7]));
       if constexpr (!TCOL) store8<DT, NTS>(a.yc + b * a.syb + r * a.sym + col, qcol[p]);
     }
   }
@@ -1138,9 +1196,16 @@ struct LaunchDual {
                     static_cast<uint32_t>(batch));
     constexpr int NT = 512;  // 256: 3 % slower at [8192, 14336]; 1024: 4 % slower
     const bool full = a.m % 128 == 0 && a.n % 128 == 0;
-    if (tcol) quant_dual_kernel<DT, FMT, NT, NTS, true, true><<<grid, NT, 0, st>>>(a);
-    else if (full) quant_dual_kernel<DT, FMT, NT, NTS, true, false><<<grid, NT, 0, st>>>(a);
-    else quant_dual_kernel<DT, FMT, NT, NTS, false, false><<<grid, NT, 0, st>>>(a);
+    // the clamp is a no-op (and is left out) at the format's largest value
+    if (a.fp8_max == fmt_max<FMT>()) return go2<NTS, false>(a, grid, full, tcol, st);
+    return go2<NTS, true>(a, grid, full, tcol, st);
+  }
+  template <bool NTS, bool CLAMP>
+  static int go2(const DualArgs& a, dim3 grid, bool full, bool tcol, hipStream_t st) {
+    constexpr int NT = 512;
+    if (tcol) quant_dual_kernel<DT, FMT, NT, NTS, true, true, CLAMP><<<grid, NT, 0, st>>>(a);
+    else if (full) quant_dual_kernel<DT, FMT, NT, NTS, true, false, CLAMP><<<grid, NT, 0, st>>>(a);
+    else quant_dual_kernel<DT, FMT, NT, NTS, false, false, CLAMP><<<grid, NT, 0, st>>>(a);
     return check_launch("quant_dual_kernel");
   }
   static int run(const DualArgs& a, int64_t batch, bool tcol, hipStream_t st) {
@@ -1460,7 +1525,10 @@ extern "C" int pcamd_selftest_fp8_convert(int fmt, uint32_t* result, void* strea
   if (fmt != kE4M3 && fmt != kE5M2) return set_error(PCAMD_ERR_INVALID, "unknown fp8 format %d", fmt);
   hipStream_t st = static_cast<hipStream_t>(stream);
   selftest_init_kernel<<<1, 1, 0, st>>>(result);
-  if (fmt == kE4M3) selftest_convert_kernel<kE4M3><<<4096, kThreads, 0, st>>>(result, 0x43E00000u);
-  else selftest_convert_kernel<kE5M2><<<4096, kThreads, 0, st>>>(result, 0x47600000u);
+  // every pattern up to the rounding midpoint above the fp8 max (464 for
+  // e4m3fn, 59392 for e5m2), which both round to the max: the quantizers
+  // leave out the clamp when x * qs cannot exceed max * (1 + 2^-23)
+  if (fmt == kE4M3) selftest_convert_kernel<kE4M3><<<4096, kThreads, 0, st>>>(result, 0x43E80000u);
+  else selftest_convert_kernel<kE5M2><<<4096, kThreads, 0, st>>>(result, 0x47680000u);
   return check_launch("selftest_convert_kernel");
 }
