@@ -97,18 +97,6 @@ PCAMD_DEV void unpack_chunk(const Chunk<DT>& c, float (&v)[8]) {
   }
 }
 
-// max |x| over the 8 elements of a chunk
-template <int DT>
-PCAMD_DEV float chunk_amax(const Chunk<DT>& c) {
-  float v[8];
-  unpack_chunk<DT>(c, v);
-  float a = fmaxf(fabsf(v[0]), fabsf(v[1]));
-  float b = fmaxf(fabsf(v[2]), fabsf(v[3]));
-  float d = fmaxf(fabsf(v[4]), fabsf(v[5]));
-  float e = fmaxf(fabsf(v[6]), fabsf(v[7]));
-  return fmaxf(fmaxf(a, b), fmaxf(d, e));
-}
-
 // bf16 pairs as raw bits: |x| clears the sign bits, and non-negative bf16
 // values order like their bit patterns, so the max of |x| over a chunk is an
 // unsigned 16-bit max (v_pk_max_u16 does two per instruction). NaN inputs are
@@ -124,6 +112,23 @@ PCAMD_DEV uint32_t max_halves(uint32_t m) { return max(m & 0xFFFFu, m >> 16); }
 // bf16 bit pattern (low 16 bits) -> float
 PCAMD_DEV float bf16_bits(uint32_t b) { return __uint_as_float(b << 16); }
 
+// max |x| over the 8 elements of a chunk
+template <int DT>
+PCAMD_DEV float chunk_amax(const Chunk<DT>& c) {
+  if constexpr (DT == kBF16) {
+    const uint32_t m = pk_max_u16(pk_max_u16(bf16_abs2(c.r[0].x), bf16_abs2(c.r[0].y)),
+                                  pk_max_u16(bf16_abs2(c.r[0].z), bf16_abs2(c.r[0].w)));
+    return bf16_bits(max_halves(m));
+  }
+  float v[8];
+  unpack_chunk<DT>(c, v);
+  float a = fmaxf(fabsf(v[0]), fabsf(v[1]));
+  float b = fmaxf(fabsf(v[2]), fabsf(v[3]));
+  float d = fmaxf(fabsf(v[4]), fabsf(v[5]));
+  float e = fmaxf(fabsf(v[6]), fabsf(v[7]));
+  return fmaxf(fmaxf(a, b), fmaxf(d, e));
+}
+
 // ---------------------------------------------------------------------------
 // wavefront reductions: max over aligned groups of LANES lanes (power of 2)
 // ---------------------------------------------------------------------------
@@ -137,21 +142,28 @@ constexpr int kDppQuadXor2 = 0x4E;     // quad_perm [2,3,0,1]
 constexpr int kDppRowHalfMirror = 0x141;
 constexpr int kDppRowMirror = 0x140;
 
-// All 64 lanes must be active when this is called.
+// All 64 lanes must be active when this is called. v >= 0 (a max of |x|):
+// non-negative floats order like their bit patterns, so the steps are
+// unsigned maxima, whose identity 0 lets each DPP move fold into its max.
 template <int LANES>
 PCAMD_DEV float group_max(float v) {
-  if constexpr (LANES >= 2) v = fmaxf(v, dpp_mov<kDppQuadXor1>(v));
-  if constexpr (LANES >= 4) v = fmaxf(v, dpp_mov<kDppQuadXor2>(v));
+  uint32_t u = __float_as_uint(v);
+  auto dpp = [](uint32_t x, auto ctrl) {
+    return max(x, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(x), decltype(ctrl)::value,
+                                                                     0xF, 0xF, false)));
+  };
+  if constexpr (LANES >= 2) u = dpp(u, std::integral_constant<int, kDppQuadXor1>{});
+  if constexpr (LANES >= 4) u = dpp(u, std::integral_constant<int, kDppQuadXor2>{});
   // after the quad steps every lane holds its quad's max; mirroring inside 8
   // (then 16) lanes pairs each quad with the other quad of the half-row (row)
-  if constexpr (LANES >= 8) v = fmaxf(v, dpp_mov<kDppRowHalfMirror>(v));
-  if constexpr (LANES >= 16) v = fmaxf(v, dpp_mov<kDppRowMirror>(v));
+  if constexpr (LANES >= 8) u = dpp(u, std::integral_constant<int, kDppRowHalfMirror>{});
+  if constexpr (LANES >= 16) u = dpp(u, std::integral_constant<int, kDppRowMirror>{});
   if constexpr (LANES >= 32) {
     // swap the two 16-lane rows of each 32-lane half (bit-mode swizzle, xor 16)
-    v = fmaxf(v, __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x401F)));
+    u = max(u, static_cast<uint32_t>(__builtin_amdgcn_ds_swizzle(static_cast<int>(u), 0x401F)));
   }
-  if constexpr (LANES >= 64) v = fmaxf(v, __shfl_xor(v, 32, 64));
-  return v;
+  if constexpr (LANES >= 64) u = max(u, static_cast<uint32_t>(__shfl_xor(static_cast<int>(u), 32, 64)));
+  return __uint_as_float(u);
 }
 
 // Unsigned max over aligned groups of LANES (<= 16) lanes. 0 is the identity
@@ -226,13 +238,14 @@ PCAMD_DEV uint32_t pack4(float a, float b, float c, float d) {
 // tl.clamp(v, -max, max)
 PCAMD_DEV float clamp_sym(float v, float hi) { return __builtin_amdgcn_fmed3f(v, -hi, hi); }
 
-// quantize a chunk: 8 elements -> 8 fp8 bytes (little-endian in a uint2)
-template <int DT, int FMT>
+// quantize a chunk: 8 elements -> 8 fp8 bytes (little-endian in a uint2);
+// CLAMP false: see quant8
+template <int DT, int FMT, bool CLAMP = true>
 PCAMD_DEV uint2 quant_chunk(const Chunk<DT>& c, float qs, float fp8_max) {
   float v[8];
   unpack_chunk<DT>(c, v);
 #pragma unroll
-  for (int i = 0; i < 8; ++i) v[i] = clamp_sym(v[i] * qs, fp8_max);
+  for (int i = 0; i < 8; ++i) v[i] = CLAMP ? clamp_sym(v[i] * qs, fp8_max) : v[i] * qs;
   return make_uint2(pack4<FMT>(v[0], v[1], v[2], v[3]), pack4<FMT>(v[4], v[5], v[6], v[7]));
 }
 

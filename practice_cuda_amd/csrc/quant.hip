@@ -90,7 +90,7 @@ PCAMD_DEV void store8(uint8_t* p, uint2 v) {
 // (units may span rows, groups never do) and no row index is needed.
 constexpr int kGroupThreads = 128;
 
-template <int DT, int FMT, int LPG, int CPL, bool NTS, bool FLAT>
+template <int DT, int FMT, int LPG, int CPL, bool NTS, bool FLAT, bool CLAMP>
 __global__ __launch_bounds__(kGroupThreads) void quant_groups_kernel(RowArgs a) {
   constexpr int EB = elem_bytes<DT>();
   const int lane = threadIdx.x & 63;
@@ -112,7 +112,7 @@ __global__ __launch_bounds__(kGroupThreads) void quant_groups_kernel(RowArgs a) 
       const Scales s = block_scales(amax, a.fp8_max, a.eps);
       if (ch < a.total) {
         if ((lane & (LPG - 1)) == 0) a.scale[ch / LPG] = s.ds;
-        store8<DT, NTS>(a.y + ch * 8, quant_chunk<DT, FMT>(cur[c], s.qs, a.fp8_max));
+        store8<DT, NTS>(a.y + ch * 8, quant_chunk<DT, FMT, CLAMP>(cur[c], s.qs, a.fp8_max));
       }
     }
     return;
@@ -137,7 +137,7 @@ __global__ __launch_bounds__(kGroupThreads) void quant_groups_kernel(RowArgs a) 
     const Scales s = block_scales(amax, a.fp8_max, a.eps);
     if (ch < a.chunks) {
       if ((lane & (LPG - 1)) == 0) srow[int64_t(ch / LPG) * a.ssn] = s.ds;
-      store8<DT, NTS>(yrow + int64_t(ch) * 8, quant_chunk<DT, FMT>(cur[c], s.qs, a.fp8_max));
+      store8<DT, NTS>(yrow + int64_t(ch) * 8, quant_chunk<DT, FMT, CLAMP>(cur[c], s.qs, a.fp8_max));
     }
   }
 }
@@ -180,7 +180,7 @@ __global__ __launch_bounds__(kThreads) void quant_waverow_kernel(RowArgs a) {
 // GRID2: grid (rows, batch), so the row and batch come from the workgroup
 // index with no division ahead of the loads; otherwise a 1-D grid of
 // batch * rows.
-template <int DT, int FMT, int CPT, bool NTS, bool GRID2>
+template <int DT, int FMT, int CPT, bool NTS, bool GRID2, bool CLAMP>
 __global__ __launch_bounds__(1024) void quant_rowblock_kernel(RowArgs a) {
   constexpr int EB = elem_bytes<DT>();
   __shared__ float red[1024 / 64];
@@ -215,7 +215,8 @@ __global__ __launch_bounds__(1024) void quant_rowblock_kernel(RowArgs a) {
 #pragma unroll
   for (int c = 0; c < CPT; ++c) {
     const int ch = t + c * nt;
-    if (ch < a.chunks) store8<DT, NTS>(yrow + int64_t(ch) * 8, quant_chunk<DT, FMT>(cur[c], s.qs, a.fp8_max));
+    if (ch < a.chunks)
+      store8<DT, NTS>(yrow + int64_t(ch) * 8, quant_chunk<DT, FMT, CLAMP>(cur[c], s.qs, a.fp8_max));
   }
 }
 
@@ -241,7 +242,7 @@ struct TileArgs {
 // m, batch) and the block comes from the workgroup index; otherwise the grid
 // is 1-D (capped) and workgroups stride over the flattened block index. FULL:
 // m and n are multiples of the block, so no row / column bounds checks.
-template <int DT, int FMT, int CPT, bool NTS, bool GRID3, bool FULL>
+template <int DT, int FMT, int CPT, bool NTS, bool GRID3, bool FULL, bool CLAMP>
 __global__ __launch_bounds__(kThreads) void quant_tile_kernel(TileArgs a) {
   constexpr int EB = elem_bytes<DT>();
   __shared__ float red[2][kThreads / 64];
@@ -274,7 +275,7 @@ __global__ __launch_bounds__(kThreads) void quant_tile_kernel(TileArgs a) {
     for (int p = 0; p < CPT; ++p) {
       const int64_t r = r0 + p * rpp + rp;
       if (FULL || (r < a.m && col < a.n))
-        store8<DT, NTS>(yb + r * a.sym + col, quant_chunk<DT, FMT>(cur[p], s.qs, a.fp8_max));
+        store8<DT, NTS>(yb + r * a.sym + col, quant_chunk<DT, FMT, CLAMP>(cur[p], s.qs, a.fp8_max));
     }
   };
   if constexpr (GRID3) {
@@ -1071,10 +1072,15 @@ template <int DT, int FMT>
 struct LaunchGroups {
   template <int LPG, int CPL, bool NTS>
   static int go(const RowArgs& a, hipStream_t st) {
+    // the clamp is a no-op (and is left out) at the format's largest value
+    return a.fp8_max == fmt_max<FMT>() ? go2<LPG, CPL, NTS, false>(a, st) : go2<LPG, CPL, NTS, true>(a, st);
+  }
+  template <int LPG, int CPL, bool NTS, bool CLAMP>
+  static int go2(const RowArgs& a, hipStream_t st) {
     constexpr int kWaves = kGroupThreads / 64;
     const int grid = static_cast<int>((int64_t(a.units) + kWaves - 1) / kWaves);
-    if (a.total > 0) quant_groups_kernel<DT, FMT, LPG, CPL, NTS, true><<<grid, kGroupThreads, 0, st>>>(a);
-    else quant_groups_kernel<DT, FMT, LPG, CPL, NTS, false><<<grid, kGroupThreads, 0, st>>>(a);
+    if (a.total > 0) quant_groups_kernel<DT, FMT, LPG, CPL, NTS, true, CLAMP><<<grid, kGroupThreads, 0, st>>>(a);
+    else quant_groups_kernel<DT, FMT, LPG, CPL, NTS, false, CLAMP><<<grid, kGroupThreads, 0, st>>>(a);
     return check_launch("quant_groups_kernel");
   }
   template <int LPG, bool NTS>
@@ -1105,11 +1111,15 @@ template <int DT, int FMT>
 struct LaunchRowBlock {
   template <int CPT, bool NTS>
   static int go(const RowArgs& a, int threads, hipStream_t st) {
+    return a.fp8_max == fmt_max<FMT>() ? go2<CPT, NTS, false>(a, threads, st) : go2<CPT, NTS, true>(a, threads, st);
+  }
+  template <int CPT, bool NTS, bool CLAMP>
+  static int go2(const RowArgs& a, int threads, hipStream_t st) {
     const uint32_t batch = a.units / a.m;
     if (batch <= 65535 && a.m <= 0x7FFFFFFFu)
-      quant_rowblock_kernel<DT, FMT, CPT, NTS, true><<<dim3(a.m, batch), threads, 0, st>>>(a);
+      quant_rowblock_kernel<DT, FMT, CPT, NTS, true, CLAMP><<<dim3(a.m, batch), threads, 0, st>>>(a);
     else
-      quant_rowblock_kernel<DT, FMT, CPT, NTS, false><<<a.units, threads, 0, st>>>(a);
+      quant_rowblock_kernel<DT, FMT, CPT, NTS, false, CLAMP><<<a.units, threads, 0, st>>>(a);
     return check_launch("quant_rowblock_kernel");
   }
   template <int MAXC, bool NTS>
@@ -1138,14 +1148,18 @@ template <int DT, int FMT>
 struct LaunchTile {
   template <int CPT, bool NTS>
   static int go(const TileArgs& a, hipStream_t st) {
+    return a.fp8_max == fmt_max<FMT>() ? go2<CPT, NTS, false>(a, st) : go2<CPT, NTS, true>(a, st);
+  }
+  template <int CPT, bool NTS, bool CLAMP>
+  static int go2(const TileArgs& a, hipStream_t st) {
     const uint32_t batch = a.blocks / (a.mb * a.nb);
     const bool full = a.m % a.block_m == 0 && a.n % (a.lpr * 8) == 0;
     if (a.mb <= 65535 && batch <= 65535) {
       const dim3 grid(a.nb, a.mb, batch);
-      if (full) quant_tile_kernel<DT, FMT, CPT, NTS, true, true><<<grid, kThreads, 0, st>>>(a);
-      else quant_tile_kernel<DT, FMT, CPT, NTS, true, false><<<grid, kThreads, 0, st>>>(a);
+      if (full) quant_tile_kernel<DT, FMT, CPT, NTS, true, true, CLAMP><<<grid, kThreads, 0, st>>>(a);
+      else quant_tile_kernel<DT, FMT, CPT, NTS, true, false, CLAMP><<<grid, kThreads, 0, st>>>(a);
     } else {
-      quant_tile_kernel<DT, FMT, CPT, NTS, false, false><<<grid_for(a.blocks), kThreads, 0, st>>>(a);
+      quant_tile_kernel<DT, FMT, CPT, NTS, false, false, CLAMP><<<grid_for(a.blocks), kThreads, 0, st>>>(a);
     }
     return check_launch("quant_tile_kernel");
   }
