@@ -871,7 +871,9 @@ PCAMD_DEV void byte_transpose4(uint32_t d0, uint32_t d1, uint32_t d2, uint32_t d
 // TCOL: the 128 x 1 output is stored transposed (element (r, c) at
 // c * ycn + r): each lane turns its 4 rows x 8 columns of fp8 bytes into 8
 // words of 4 rows (byte transposes), the block passes through 16 KiB of LDS,
-// and the transposed rows leave as 16-byte stores. Needs whole blocks. Each
+// and the transposed rows leave as 16-byte stores (ycn a multiple of 16);
+// in a partial block the 16 rows of a piece that straddle m go out byte by
+// byte and columns past n are skipped. Each
 // row's 128 columns sit in one aligned 16-lane row of the wave (DPP max);
 // column maxima meet through lane shuffles, then LDS across the waves. The
 // results are those of the 1 x 128 and 128 x 1 quantizers run separately.
@@ -889,7 +891,7 @@ __global__ __launch_bounds__(NT) void quant_dual_kernel(DualArgs a) {
   constexpr int EB = elem_bytes<DT>();
   constexpr int CPT = 2048 / NT, WAVES = NT / 64, RPP = NT / 16;
   constexpr bool PK = DT == kBF16 && CPT == 4;
-  static_assert(!TCOL || (FULL && CPT == 4), "transposed column output: whole blocks, four rows per lane");
+  static_assert(!TCOL || CPT == 4, "transposed column output: four rows per lane");
   __shared__ float part[WAVES][128];  // PK: [WAVES][64] packed column-pair maxima
   __shared__ float qsv[128];
   // transposed block: 128 columns x 32 words of 4 rows; the 16-byte groups of
@@ -1002,6 +1004,7 @@ __global__ __launch_bounds__(NT) void quant_dual_kernel(DualArgs a) {
 #pragma unroll
   for (int p = 0; p < CPT; ++p) {
     const int64_t r = row_of(p);
+    qcol[p] = make_uint2(0u, 0u);
     if (FULL || (r < a.m && col < a.n)) {
       float v[8];
       unpack_chunk<DT>(raw[p], v);
@@ -1025,14 +1028,23 @@ __global__ __launch_bounds__(NT) void quant_dual_kernel(DualArgs a) {
     }
     __syncthreads();
     uint8_t* ycb = a.yc + b * a.ycb + (strip * 128) * a.ycn + r0;
+    const int64_t rows = FULL ? 128 : min(int64_t(128), a.m - r0);  // valid rows of the block
 #pragma unroll
     for (int j = 0; j < 1024 / NT; ++j) {
       const int q = t + j * NT;           // 16-byte piece: column q / 8, rows 16 (q % 8) .. + 15
       const int ct = q >> 3, seg = q & 7;
       const u32x4_t v = *reinterpret_cast<const u32x4_t*>(tt + ct * 32 + ((seg ^ ((ct >> 3) & 7)) << 2));
       uint8_t* dst = ycb + ct * a.ycn + seg * 16;
-      if constexpr (NTS) __builtin_nontemporal_store(v, reinterpret_cast<u32x4_t*>(dst));
-      else *reinterpret_cast<u32x4_t*>(dst) = v;
+      if (FULL || (strip * 128 + ct < a.n && 16 * seg + 16 <= rows)) {
+        if constexpr (NTS) __builtin_nontemporal_store(v, reinterpret_cast<u32x4_t*>(dst));
+        else *reinterpret_cast<u32x4_t*>(dst) = v;
+      } else if (strip * 128 + ct < a.n) {
+        // the piece straddling row m: its first rows - 16 seg bytes
+        const uint32_t wv[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int k = 0; k < 16; ++k)
+          if (16 * seg + k < rows) dst[k] = static_cast<uint8_t>(wv[k >> 2] >> (8 * (k & 3)));
+      }
     }
   }
 }
@@ -1217,7 +1229,8 @@ struct LaunchDual {
   template <bool NTS, bool CLAMP>
   static int go2(const DualArgs& a, dim3 grid, bool full, bool tcol, hipStream_t st) {
     constexpr int NT = 512;
-    if (tcol) quant_dual_kernel<DT, FMT, NT, NTS, true, true, CLAMP><<<grid, NT, 0, st>>>(a);
+    if (tcol && full) quant_dual_kernel<DT, FMT, NT, NTS, true, true, CLAMP><<<grid, NT, 0, st>>>(a);
+    else if (tcol) quant_dual_kernel<DT, FMT, NT, NTS, false, true, CLAMP><<<grid, NT, 0, st>>>(a);
     else if (full) quant_dual_kernel<DT, FMT, NT, NTS, true, false, CLAMP><<<grid, NT, 0, st>>>(a);
     else quant_dual_kernel<DT, FMT, NT, NTS, false, false, CLAMP><<<grid, NT, 0, st>>>(a);
     return check_launch("quant_dual_kernel");
@@ -1421,9 +1434,9 @@ extern "C" int pcamd_quant_block_dual(const void* x, int x_dtype, int64_t batch,
   const bool fast = row_fast_ok(x, x_dtype, y_row, n, sxb, sxm, sxn, syb, sym, syn) && block == 128 &&
                     batch <= 65535 && (m + 127) / 128 <= 65535 && (n + 127) / 128 <= INT32_MAX;
   const bool same_layout = ycb == syb && ycm == sym && ycn == syn && aligned(y_col, 8);
-  // transposed 128 x 1 output (element (r, c) at c * ycn + r): whole blocks, 16-byte aligned rows
-  const bool transposed = ycm == 1 && ycn >= m && m % 128 == 0 && n % 128 == 0 && ycn % 16 == 0 &&
-                          ycb % 16 == 0 && aligned(y_col, 16);
+  // transposed 128 x 1 output (element (r, c) at c * ycn + r), 16-byte aligned rows
+  const bool transposed = ycm == 1 && ycn >= m && ycn % 16 == 0 && (batch == 1 || ycb % 16 == 0) &&
+                          aligned(y_col, 16);
   if (fast && (same_layout || transposed)) {
     DualArgs a{};
     a.x = static_cast<const char*>(x);

@@ -91,8 +91,9 @@ def hip_per_block_quant_dual(
     dim for the forward / dgrad GEMMs, block x 1 groups along the rows for
     wgrad. The results are bit-identical to the two separate calls.
     col_transposed: the block x 1 result is stored transposed (a [.., N, M]
-    contiguous buffer seen as [.., M, N]), so a GEMM that reduces over M reads
-    it K-major.
+    buffer seen as [.., M, N]), so a GEMM that reduces over M reads it
+    K-major; its rows are padded to a multiple of 16 bytes (row pitch
+    ceil(M / 16) * 16), which the kernel's 16-byte transposed stores need.
     """
     if x.ndim not in (2, 3):
         raise ValueError(f"per-block quant expects a 2D or 3D tensor, got {tuple(x.shape)}")
@@ -103,8 +104,9 @@ def hip_per_block_quant_dual(
 
     out_row = torch.empty_like(x, dtype=fp8_dtype, memory_format=torch.preserve_format)
     if col_transposed:
-        out_col = torch.empty(*x.shape[:-2], x.shape[-1], x.shape[-2], dtype=fp8_dtype,
-                              device=x.device).transpose(-1, -2)
+        pitch = -(-x.shape[-2] // 16) * 16
+        out_col = torch.empty(*x.shape[:-2], x.shape[-1], pitch, dtype=fp8_dtype,
+                              device=x.device)[..., :x.shape[-2]].transpose(-1, -2)
     else:
         out_col = torch.empty_strided(out_row.shape, out_row.stride(), dtype=fp8_dtype, device=x.device)
     batch, m, n, xs, ys = C.dims3(x, out_row)

@@ -139,8 +139,9 @@ def quant_block_dual(x: torch.Tensor, block: int, fp8_dtype: torch.dtype,
                      eps: float) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
     """``quant_block(x, 1, block)`` and ``quant_block(x, block, 1)`` from one read
     of x: (fp8 1 x block, its scales [B, M, ceil(N/block)], fp8 block x 1 stored
-    transposed (a [B, N, M] buffer seen as [B, M, N], the K-major operand of a
-    GEMM reducing over M), its scales [B, ceil(M/block), N])."""
+    transposed (a [B, N, M] buffer with rows padded to 16 bytes, seen as
+    [B, M, N]: the K-major operand of a GEMM reducing over M), its scales
+    [B, ceil(M/block), N])."""
     r, c = hip_per_block_quant_dual(x, block=block, fp8_dtype=fp8_dtype, eps=eps, col_transposed=True)
     return r.tensor, r.dequant_scale, c.tensor, c.dequant_scale
 
@@ -149,7 +150,7 @@ def quant_block_dual(x: torch.Tensor, block: int, fp8_dtype: torch.dtype,
 def _(x, block, fp8_dtype, eps):
     b, m, n = x.shape
     return (torch.empty_like(x, dtype=fp8_dtype), x.new_empty((b, m, -(-n // block)), dtype=torch.float32),
-            x.new_empty((b, n, m), dtype=fp8_dtype).transpose(-1, -2),
+            x.new_empty((b, n, -(-m // 16) * 16), dtype=fp8_dtype)[..., :m].transpose(-1, -2),
             x.new_empty((b, -(-m // block), n), dtype=torch.float32))
 
 

@@ -236,6 +236,8 @@ DUAL_CASES = [
     ((384, 256), "bf16", 128, "e4m3", "transposed"),  # column-major input: the two quantizers in turn
     ((256, 384), "bf16", 128, "e4m3", "zero_rows"),
     ((2, 256, 384), "bf16", 128, "e4m3", "padded"),   # row pitch 640 (a column slice)
+    ((2, 333, 264), "bf16", 128, "e5m2", None),       # partial last row group in a batch, partial strip
+    ((1000, 256), "bf16", 128, "e4m3", None),         # partial last row group, several 16-row pieces cut
 ]
 
 
@@ -258,7 +260,8 @@ def test_dual_matches_oracle(dev, shape, dtype, block, fmt, kind, col_t):
     print(f"dual shape={shape} dtype={dtype} block={block} fmt={fmt} kind={kind} col_t={col_t}", flush=True)
     r_row, r_col = hip_per_block_quant_dual(xd, block=block, fp8_dtype=FMT[fmt], col_transposed=col_t)
     if col_t:
-        assert r_col.tensor.stride(-2) == 1 and r_col.tensor.stride(-1) == shape[-2]
+        # [.., N, M] storage, rows padded to 16 bytes
+        assert r_col.tensor.stride(-2) == 1 and r_col.tensor.stride(-1) == -(-shape[-2] // 16) * 16
     q1, s1 = O.quant_block(x, 1, block, fmt=fmt)
     q2, s2 = O.quant_block(x, block, 1, fmt=fmt)
     assert r_row.meta["block_m"] == 1 and r_row.meta["block_n"] == block
