@@ -32,7 +32,7 @@ sys.path.insert(0, ROOT)
 HBM_PEAK_GBS = 8000.0        # MI355X HBM3E
 # the kernel pcamd_quant_channel launches for the headline workload (rows of
 # 7168 bf16 elements: one 256-thread workgroup per row, up to 4 chunks per thread)
-HEADLINE_KERNEL = "quant_rowblock_kernel<bf16,e4m3,4,nt,grid2> (256 threads)"
+HEADLINE_KERNEL = "quant_rowblock_kernel<bf16,e4m3,4,nt,grid2,noclamp> (256 threads)"
 FP8_PEAK_TFLOPS = 5000.0     # MI355X dense fp8 MFMA (5.0 PFLOP/s)
 SETTLE_MS = 100.0            # untimed load before the first (headline) measurement
 # the kernels configs 4 and 5 launch (as rocprofv3 names them), to match the

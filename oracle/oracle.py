@@ -159,12 +159,13 @@ def decode(q: np.ndarray, fmt="e4m3") -> np.ndarray:
 
 
 def quant_block(x, block_m: int, block_n: int, fmt="e4m3", eps: float = 1e-12,
-                dtype: Optional[str] = None, threads: int = 1):
+                dtype: Optional[str] = None, threads: int = 1,
+                fp8_max: Optional[float] = None):
     """Per-block quantization; returns (q uint8 [.., m, n], scale fp32).
 
     The scale has the reference's shape: [m_blocks, n_blocks] for 2D input
     (``impls/triton_per_block.py:96-100,138``) and [b, m_blocks, n_blocks]
-    for 3D input.
+    for 3D input. fp8_max defaults to the format's largest finite value.
     """
     arr, xd = as_bits(x, dtype)
     b, m, n, sxb, sxm, sxn = _dims(arr)
@@ -175,7 +176,7 @@ def quant_block(x, block_m: int, block_n: int, fmt="e4m3", eps: float = 1e-12,
     rc = lib().oracle_quant_block(
         arr.ctypes.data, xd, b, m, n, sxb, sxm, sxn, q.ctypes.data, code,
         m * n, n, 1, s.ctypes.data, mb * nb, nb, 1, block_m, block_n,
-        FP8_MAX[code], eps, threads)
+        FP8_MAX[code] if fp8_max is None else fp8_max, eps, threads)
     if rc != 0:
         raise ValueError("oracle_quant_block rejected its arguments")
     if arr.ndim == 2:
@@ -184,7 +185,8 @@ def quant_block(x, block_m: int, block_n: int, fmt="e4m3", eps: float = 1e-12,
 
 
 def quant_channel(x, channel_axis: int = -1, fmt="e4m3", eps: float = 1e-12,
-                  dtype: Optional[str] = None, threads: int = 1):
+                  dtype: Optional[str] = None, threads: int = 1,
+                  fp8_max: Optional[float] = None):
     """Per-channel quantization; scale [channels] (2D) or [b, channels]."""
     arr, xd = as_bits(x, dtype)
     b, m, n, sxb, sxm, sxn = _dims(arr)
@@ -194,7 +196,8 @@ def quant_channel(x, channel_axis: int = -1, fmt="e4m3", eps: float = 1e-12,
     s = np.empty((b, ch), dtype=np.float32)
     rc = lib().oracle_quant_channel(
         arr.ctypes.data, xd, b, m, n, sxb, sxm, sxn, q.ctypes.data, code,
-        m * n, n, 1, s.ctypes.data, ch, 1, channel_axis, FP8_MAX[code], eps, threads)
+        m * n, n, 1, s.ctypes.data, ch, 1, channel_axis,
+        FP8_MAX[code] if fp8_max is None else fp8_max, eps, threads)
     if rc != 0:
         raise ValueError("oracle_quant_channel rejected its arguments")
     if arr.ndim == 2:

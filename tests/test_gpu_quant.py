@@ -421,3 +421,118 @@ def test_torch_compile_role_same_bytes(dev, axis):
     assert torch.equal(a.dequant_scale, b.dequant_scale)
     assert a.impl == "torch_compile_per_channel" and a.meta["quant_strategy"] == "torch_compile"
     assert a.granularity == "channel" and a.meta["channel_axis"] == axis
+
+
+# ---------------------------------------------------------------------------
+# fp8_max below the format maximum: the clamping kernel instantiations
+# ---------------------------------------------------------------------------
+def _clamp_witnesses(fmax: float) -> np.ndarray:
+    """bf16 values s in [1, 8) with fl(s * fl(fmax / s)) > fmax in fp32: as a
+    block's amax, s quantizes to a product just above fmax, so a kernel that
+    skipped the clamp would round it one code too far when fmax sits on a
+    rounding midpoint."""
+    s = (np.arange(0x3F80, 0x4100, dtype=np.uint32) << 16).view(np.float32)
+    f = np.float32(fmax)
+    return s[s * (f / s) > f]
+
+
+def _planted_input(shape, dtype, fmax, seed):
+    """N(0, 0.3) clipped to |x| < 1, one witness of random sign per row."""
+    g = np.random.default_rng(seed)
+    x = np.clip(g.standard_normal(shape) * 0.3, -0.99, 0.99).astype(np.float32)
+    w = _clamp_witnesses(fmax)
+    rows = x.reshape(-1, shape[-1])
+    cols = g.integers(0, shape[-1], rows.shape[0])
+    rows[np.arange(rows.shape[0]), cols] = w[g.integers(0, len(w), rows.shape[0])] * g.choice([-1.0, 1.0], rows.shape[0])
+    return torch.from_numpy(x).to(DT[dtype])
+
+
+def _abi_quant_block(xd, bm, bn, fp8, fmax):
+    y = torch.empty_like(xd, dtype=fp8)
+    x3, y3 = (xd[None], y[None]) if xd.ndim == 2 else (xd, y)
+    b, m, n = x3.shape
+    s = torch.empty(b, -(-m // bm), -(-n // bn), device=xd.device)
+    _lib.check(_lib.lib().pcamd_quant_block(
+        _lib.ptr(x3), _lib.dtype_code(xd.dtype), b, m, n, *x3.stride(), _lib.ptr(y3), _lib.dtype_code(fp8),
+        *y3.stride(), _lib.ptr(s), *s.stride(), bm, bn, float(fmax), 1e-12, _lib.stream_of(xd)), "quant_block")
+    return y, s
+
+
+def _abi_quant_dual(xd, fp8, fmax, transposed):
+    x3 = xd[None] if xd.ndim == 2 else xd
+    b, m, n = x3.shape
+    yr = torch.empty_like(x3, dtype=fp8)
+    if transposed:
+        pitch = -(-m // 16) * 16
+        yc = torch.empty(b, n, pitch, dtype=fp8, device=xd.device)[..., :m].transpose(-1, -2)
+    else:
+        yc = torch.empty_like(yr)
+    sr = torch.empty(b, m, -(-n // 128), device=xd.device)
+    sc = torch.empty(b, -(-m // 128), n, device=xd.device)
+    _lib.check(_lib.lib().pcamd_quant_block_dual(
+        _lib.ptr(x3), _lib.dtype_code(xd.dtype), b, m, n, *x3.stride(), _lib.ptr(yr), *yr.stride(),
+        _lib.ptr(yc), *yc.stride(), _lib.dtype_code(fp8), _lib.ptr(sr), *sr.stride(), _lib.ptr(sc),
+        *sc.stride(), 128, float(fmax), 1e-12, _lib.stream_of(xd)), "quant_block_dual")
+    return yr, sr, yc, sc
+
+
+def _abi_quant_channel(xd, axis, fp8, fmax):
+    y = torch.empty_like(xd, dtype=fp8)
+    x3, y3 = (xd[None], y[None]) if xd.ndim == 2 else (xd, y)
+    b, m, n = x3.shape
+    s = torch.empty(b, m if axis == -2 else n, device=xd.device)
+    _lib.check(_lib.lib().pcamd_quant_channel(
+        _lib.ptr(x3), _lib.dtype_code(xd.dtype), b, m, n, *x3.stride(), _lib.ptr(y3), _lib.dtype_code(fp8),
+        *y3.stride(), _lib.ptr(s), *s.stride(), axis, float(fmax), 1e-12, _lib.stream_of(xd)), "quant_channel")
+    return y, s
+
+
+def _same_bits(q, s, q_ref, s_ref, label):
+    torch.cuda.synchronize()
+    qg = qbits(q).reshape(np.asarray(q_ref).shape)
+    assert np.array_equal(qg, q_ref), f"{label}: {int((qg != q_ref).sum())} fp8 bytes differ"
+    sr = np.asarray(s_ref, np.float32).reshape(-1).view(np.uint32)
+    assert np.array_equal(sbits(s), sr), f"{label}: scales differ"
+
+
+# (fmt, fp8_max): e4m3 just below the 240/256 midpoint and on the 96/104
+# midpoint, e5m2 on the 32768/40960 midpoint
+REDUCED_MAX = [("e4m3", float(np.nextafter(np.float32(248.0), np.float32(0.0)))), ("e4m3", 100.0),
+               ("e5m2", 36864.0)]
+REDUCED_PATHS = [
+    # (kind, shape, dtype, bm, bn)
+    ("block", (64, 1024), "bf16", 1, 128),        # row groups, flat
+    ("block", (3, 40, 1000), "f32", 1, 128),      # row groups, ragged
+    ("block", (256, 384), "bf16", 128, 128),      # tiles, whole
+    ("block", (200, 300), "f16", 128, 128),       # tiles, partial
+    ("block", (300, 256), "bf16", 128, 1),        # column groups
+    ("block", (50, 70), "f16", 4, 16),            # generic
+    ("channel-2", (64, 2048), "bf16", 0, 0),      # register-resident rows
+    ("channel-1", (256, 512), "bf16", 0, 0),      # column strips
+    ("dual", (256, 512), "bf16", 0, 0),
+    ("dual", (2, 333, 264), "bf16", 0, 0),
+    ("dual_t", (256, 512), "bf16", 0, 0),
+    ("dual_t", (1000, 256), "bf16", 0, 0),
+]
+
+
+@pytest.mark.parametrize("fmt,fmax", REDUCED_MAX, ids=["e4m3_248m", "e4m3_100", "e5m2_36864"])
+@pytest.mark.parametrize("kind,shape,dtype,bm,bn", REDUCED_PATHS)
+def test_reduced_fp8_max_matches_oracle(dev, kind, shape, dtype, bm, bn, fmt, fmax):
+    print(f"reduced fp8_max {kind} shape={shape} dtype={dtype} {bm}x{bn} {fmt} fp8_max={fmax!r}", flush=True)
+    x = _planted_input(shape, dtype, fmax, seed=sum(shape) + bm + bn)
+    xd = x.to(dev)
+    fp8 = FMT[fmt]
+    if kind == "block":
+        q, s = _abi_quant_block(xd, bm, bn, fp8, fmax)
+        _same_bits(q, s, *O.quant_block(x, bm, bn, fmt=fmt, fp8_max=fmax), kind)
+    elif kind.startswith("channel"):
+        axis = int(kind[len("channel"):])
+        q, s = _abi_quant_channel(xd, axis, fp8, fmax)
+        _same_bits(q, s, *O.quant_channel(x, axis, fmt=fmt, fp8_max=fmax), kind)
+    else:
+        yr, sr, yc, sc = _abi_quant_dual(xd, fp8, fmax, kind == "dual_t")
+        q1, s1 = O.quant_block(x, 1, 128, fmt=fmt, fp8_max=fmax)
+        q2, s2 = O.quant_block(x, 128, 1, fmt=fmt, fp8_max=fmax)
+        _same_bits(yr, sr, q1, s1, kind + " rows")
+        _same_bits(yc, sc, q2, s2, kind + " columns")

@@ -160,6 +160,28 @@ def test_output_range(fmt, fmax):
         assert np.all(np.isfinite(v)) and np.abs(v).max() <= fmax
 
 
+def test_reduced_fp8_max_clamps_before_rounding():
+    """With fp8_max F just below the 240/256 rounding midpoint (248), an amax
+    s whose product fl(s * fl(F / s)) lands above F must encode as 240 (clamp
+    to F, then round) and not as 256 (round the unclamped product)."""
+    F = np.nextafter(f32(248.0), f32(0.0))
+    s = _find_amax(lambda v: v * (F / v) > F)
+    x = np.zeros((2, 128), np.float32)
+    x[0, 0], x[1, 5] = s, -s
+    prod = s * (F / s)
+    assert O.encode(np.array([prod], np.float32))[0] == 0x78       # 256 unclamped
+    for q in (O.quant_block(x, 1, 128, fp8_max=float(F))[0],
+              O.quant_channel(x, -2, fp8_max=float(F))[0]):
+        assert q[0, 0] == 0x77 and q[1, 5] == 0xF7                  # +-240
+    # F = 100 is the 96/104 midpoint and ties to 96: after the clamp every
+    # code decodes to at most 96, and the amax element reaches it
+    xr = np.random.default_rng(5).standard_normal((40, 300)).astype(np.float32)
+    for q in (O.quant_block(xr, 1, 128, fp8_max=100.0)[0], O.quant_block(xr, 128, 128, fp8_max=100.0)[0],
+              O.quant_channel(xr, -1, fp8_max=100.0)[0]):
+        v = np.abs(O.decode(q))
+        assert v.max() == 96.0
+
+
 def test_reciprocal_factor_closed_form():
     # reference fp8_quant_test.py:94-103: dequant scale == amax / 448 (rtol 1e-5)
     x = np.random.default_rng(2).standard_normal((32, 2048)).astype(np.float32)
