@@ -74,6 +74,10 @@ def parse():
     p.add_argument("--pmc-probe", action="store_true",
                    help="eager launches for rocprofv3 --pmc passes: 3 plain bf16 copies of "
                         "256 MiB (calibration) then 3 config-2 quantizations")
+    p.add_argument("--gemm-ref", choices=["graph", "eager"], default=None,
+                   help="the config-5 GEMM shapes with tensor and row/column scales, this build's kernels "
+                        "next to hipBLASLt (torch._scaled_mm): 'graph' times them (HIP graphs, one JSON "
+                        "line), 'eager' launches each 3 times for rocprofv3 passes")
     return p.parse_args()
 
 
@@ -699,6 +703,78 @@ def pmc_probe_bmm(torch, dev):
                       "order": ["copy x3", "config4 x3"] + [f"{k} x3" for k in gemms]}))
 
 
+def gemm_ref(torch, dev, steps, warmup, eager):
+    """Reference point for the config-5 GEMMs: the same three products with
+    per-tensor scales and the forward with row / column scales, run by this
+    build's kernels and by hipBLASLt through torch._scaled_mm (which takes
+    no 1x128 / 128x128 block scales, so the block-scaled trio has no library
+    counterpart). Both sides use the same fp8 operands and scales; their
+    outputs are compared (max-abs-rel). 'graph': median HIP-graph time per
+    launch, one JSON line; 'eager': three launches of each, for counters."""
+    from practice_cuda_amd.impls.hip_per_channel import hip_per_channel_bmm, hip_per_channel_quant
+    from practice_cuda_amd.impls.hip_per_tensor import hip_per_tensor_bmm, hip_per_tensor_quant
+    from practice_cuda_amd.registry import QuantResult
+    M, K, N = 8192, 4096, 14336
+    g = torch.Generator().manual_seed(0)
+    X = torch.randn(M, K, generator=g).bfloat16().to(dev)
+    W = (torch.randn(N, K, generator=g) * 0.02).bfloat16().to(dev)
+    dY = (torch.randn(M, N, generator=g) * 1e-3).bfloat16().to(dev)
+    tx, tw, tdy = (hip_per_tensor_quant(t[None]) for t in (X, W, dY))
+
+    def view(r, t):
+        return QuantResult(t, r.dequant_scale, r.impl, r.granularity, dict(r.meta))
+
+    bf = torch.bfloat16
+    sx, sw, sdy = (r.dequant_scale.reshape(()).float() for r in (tx, tw, tdy))
+    x8, w8, dy8 = tx.tensor[0], tw.tensor[0], tdy.tensor[0]
+    w_cm = w8.t().contiguous().t()               # [N, K] column-major
+    dyt8 = dy8.t().contiguous()                  # [N, M] row-major
+    x_cm = x8.t().contiguous().t()               # [M, K] column-major
+    out_f = torch.empty(1, M, N, dtype=bf, device=dev)
+    out_d = torch.empty(1, M, K, dtype=bf, device=dev)
+    out_w = torch.empty(1, N, K, dtype=bf, device=dev)
+    a_w, b_w = view(tdy, dyt8[None]), view(tx, x_cm[None])    # wgrad on K-major operands
+    cx = hip_per_channel_quant(X[None], channel_axis=-2)
+    cw = hip_per_channel_quant(W[None], channel_axis=-2)
+    cwt = QuantResult(cw.tensor.transpose(-1, -2), cw.dequant_scale, cw.impl, "channel",
+                      {**cw.meta, "channel_axis": -1})
+    csa = cx.dequant_scale.reshape(M, 1).contiguous()
+    csb = cw.dequant_scale.reshape(1, N).contiguous()
+    cases = {
+        "tensor_fwd": (lambda i: hip_per_tensor_bmm(tx, view(tw, tw.tensor.transpose(-1, -2)), out=out_f),
+                       lambda i: torch._scaled_mm(x8, w8.t(), scale_a=sx, scale_b=sw, out_dtype=bf)),
+        "tensor_dgrad": (lambda i: hip_per_tensor_bmm(tdy, tw, out=out_d),
+                         lambda i: torch._scaled_mm(dy8, w_cm, scale_a=sdy, scale_b=sw, out_dtype=bf)),
+        "tensor_wgrad": (lambda i: hip_per_tensor_bmm(a_w, b_w, out=out_w),
+                         lambda i: torch._scaled_mm(dyt8, x_cm, scale_a=sdy, scale_b=sx, out_dtype=bf)),
+        "channel_fwd": (lambda i: hip_per_channel_bmm(cx, cwt, out=out_f),
+                        lambda i: torch._scaled_mm(cx.tensor[0], cw.tensor[0].t(),
+                                                   scale_a=csa, scale_b=csb, out_dtype=bf)),
+    }
+    flops = 2 * M * N * K
+    res = {}
+    for name, (ours, lib) in cases.items():
+        if eager:
+            for fn in (ours, lib):
+                for i in range(3):
+                    fn(i)
+                torch.cuda.synchronize()
+            continue
+        o = ours(0)
+        a = o.float().reshape(-1, o.shape[-1])
+        b = lib(0).float()
+        rel = ((a - b).abs().max() / b.abs().max()).item()
+        del a, b
+        row = {"max_abs_rel_vs_hipblaslt": rel}
+        for side, fn in (("ours", ours), ("hipblaslt", lib)):
+            ms, _ = graph_time(torch, fn, steps, warmup)
+            row[side] = {"ms": ms, "TFLOP/s": flops / (ms * 1e-3) / 1e12}
+        res[name] = row
+    if not eager:
+        print(json.dumps({"gemm_ref": res, "shape": {"M": M, "K": K, "N": N},
+                          "note": "fwd X W^T, dgrad dY W, wgrad dY^T X on K-major operands"}))
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -717,6 +793,9 @@ def main():
         return
     if args.pmc_probe_bmm:
         pmc_probe_bmm(torch, dev)
+        return
+    if args.gemm_ref:
+        gemm_ref(torch, dev, args.steps, args.warmup, args.gemm_ref == "eager")
         return
 
     x2 = make_config2(torch)

@@ -34,6 +34,7 @@
 #include <algorithm>
 #include <cstdint>
 #include <cstdlib>
+#include <type_traits>
 
 #include "abi_util.h"
 #include "bmm_fast.h"
@@ -355,39 +356,50 @@ __global__ __launch_bounds__(NT) void bmm_kernel(Args a) {
   }
 
   // ---- epilogue: scales, then bf16 fast path or the general path ----
-  float tscale = 1.0f;
-  if constexpr (MODE == kTensor) tscale = a.scales_are_quant ? 1.0f / (a.sa[0] * a.sb[0]) : a.sa[0];
-  const bool plain = a.bias == nullptr && a.act == PCAMD_ACT_NONE && a.c_dtype == kBF16;
+  // SAQ (scales_are_quant, channel mode): 1 / (sa * sb) per element, a
+  // compile-time branch so that the other case carries no division
+  auto epilogue = [&](auto saq_c) {
+    constexpr bool SAQ = decltype(saq_c)::value;
+    float tscale = 1.0f;
+    if constexpr (MODE == kTensor) tscale = a.scales_are_quant ? 1.0f / (a.sa[0] * a.sb[0]) : a.sa[0];
+    const bool plain = a.bias == nullptr && a.act == PCAMD_ACT_NONE && a.c_dtype == kBF16;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int64_t mm = m0 + wm * 64 + i * 16 + lr;
-    float sam_v = 1.0f;
-    if constexpr (MODE == kChannel) sam_v = mm < a.m ? a.sa[bidx * a.ssab + mm * a.ssa1] : 0.0f;
+    for (int i = 0; i < 4; ++i) {
+      const int64_t mm = m0 + wm * 64 + i * 16 + lr;
+      float sam_v = 1.0f;
+      if constexpr (MODE == kChannel) sam_v = mm < a.m ? a.sa[bidx * a.ssab + mm * a.ssa1] : 0.0f;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int64_t nn = n0 + wn * 64 + j * 16 + 4 * lg;
-      float v[4];
+      for (int j = 0; j < 4; ++j) {
+        const int64_t nn = n0 + wn * 64 + j * 16 + 4 * lg;
+        float v[4];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        float x = acc[i][j][r];
-        if constexpr (MODE == kChannel) {
-          float s = nn + r < a.n ? sam_v * a.sb[bidx * a.ssbb + (nn + r) * a.ssb1] : 0.0f;
-          if (a.scales_are_quant) s = 1.0f / s;
-          x *= s;
-        } else if constexpr (MODE == kTensor) {
-          x *= tscale;
+        for (int r = 0; r < 4; ++r) {
+          float x = acc[i][j][r];
+          if constexpr (MODE == kChannel) {
+            float s = nn + r < a.n ? sam_v * a.sb[bidx * a.ssbb + (nn + r) * a.ssb1] : 0.0f;
+            if constexpr (SAQ) s = 1.0f / s;
+            x *= s;
+          } else if constexpr (MODE == kTensor) {
+            x *= tscale;
+          }
+          v[r] = x;
         }
-        v[r] = x;
-      }
-      if (mm >= a.m || nn >= a.n) continue;
-      __bf16* p = reinterpret_cast<__bf16*>(a.c) + bidx * a.scb + mm * a.scm + nn;
-      if (plain && nn + 4 <= a.n && (reinterpret_cast<uintptr_t>(p) & 7) == 0) {
-        *reinterpret_cast<uint2*>(p) = make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
-      } else {
-        const int nvalid = static_cast<int>(min(static_cast<int64_t>(4), a.n - nn));
-        epilogue_general(a, bidx, mm, nn, nvalid, v[0], v[1], v[2], v[3]);
+        if (mm >= a.m || nn >= a.n) continue;
+        __bf16* p = reinterpret_cast<__bf16*>(a.c) + bidx * a.scb + mm * a.scm + nn;
+        if (plain && nn + 4 <= a.n && (reinterpret_cast<uintptr_t>(p) & 7) == 0) {
+          *reinterpret_cast<uint2*>(p) = make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
+        } else {
+          const int nvalid = static_cast<int>(min(static_cast<int64_t>(4), a.n - nn));
+          epilogue_general(a, bidx, mm, nn, nvalid, v[0], v[1], v[2], v[3]);
+        }
       }
     }
+  };
+  if constexpr (MODE == kChannel) {
+    if (a.scales_are_quant) epilogue(std::true_type{});
+    else epilogue(std::false_type{});
+  } else {
+    epilogue(std::false_type{});
   }
 }
 

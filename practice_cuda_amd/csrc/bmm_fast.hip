@@ -29,6 +29,7 @@
 
 #include <algorithm>
 #include <cstdint>
+#include <type_traits>
 
 #include "abi_util.h"
 #include "bmm_epilogue.h"
@@ -407,56 +408,67 @@ __global__ __launch_bounds__(NT, 1) void bmm_fast_kernel(FastArgs a) {
   }
 
   // ---- epilogue ----
-  float tscale = 1.0f;
-  if constexpr (MODE == 2) tscale = a.scales_are_quant ? 1.0f / (a.sa[0] * a.sb[0]) : a.sa[0];
-  const bool plain = a.bias == nullptr && a.act == PCAMD_ACT_NONE && a.c_dtype == kBF16;
-  float sam[4];
+  // SAQ (scales_are_quant, channel mode): 1 / (sa * sb) per element, a
+  // compile-time branch so that the other case carries no division
+  auto epilogue = [&](auto saq_c) {
+    constexpr bool SAQ = decltype(saq_c)::value;
+    float tscale = 1.0f;
+    if constexpr (MODE == 2) tscale = a.scales_are_quant ? 1.0f / (a.sa[0] * a.sb[0]) : a.sa[0];
+    const bool plain = a.bias == nullptr && a.act == PCAMD_ACT_NONE && a.c_dtype == kBF16;
+    float sam[4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int mm = row_base + 16 * i;
-    sam[i] = 1.0f;
-    if constexpr (MODE == 1) sam[i] = mm < a.m ? a.sa[bidx * a.ssab + int64_t(mm) * a.ssa1] : 0.0f;
-  }
-  auto value = [&](int i, int j, float (&v)[4]) {
-    const int nn = col_base + 16 * j;
+    for (int i = 0; i < 4; ++i) {
+      const int mm = row_base + 16 * i;
+      sam[i] = 1.0f;
+      if constexpr (MODE == 1) sam[i] = mm < a.m ? a.sa[bidx * a.ssab + int64_t(mm) * a.ssa1] : 0.0f;
+    }
+    auto value = [&](int i, int j, float (&v)[4]) {
+      const int nn = col_base + 16 * j;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      float x = acc[i][j][r];
-      if constexpr (MODE == 1) {
-        float s = nn + r < a.n ? sam[i] * a.sb[bidx * a.ssbb + int64_t(nn + r) * a.ssb1] : 0.0f;
-        if (a.scales_are_quant) s = 1.0f / s;
-        x *= s;
-      } else if constexpr (MODE == 2) {
-        x *= tscale;
+      for (int r = 0; r < 4; ++r) {
+        float x = acc[i][j][r];
+        if constexpr (MODE == 1) {
+          float s = nn + r < a.n ? sam[i] * a.sb[bidx * a.ssbb + int64_t(nn + r) * a.ssb1] : 0.0f;
+          if constexpr (SAQ) s = 1.0f / s;
+          x *= s;
+        } else if constexpr (MODE == 2) {
+          x *= tscale;
+        }
+        v[r] = x;
       }
-      v[r] = x;
+    };
+    if (staged_output_ok(a.c, a.scb, a.scm, a.n, plain)) {
+      // the stage the last K step did not read is free (every wave passed the
+      // last barrier after its final read of it): 8 KiB of it per wave
+      store_subtile_staged(smem + (ksteps & 1) * STAGE + wave * 8192, reinterpret_cast<__bf16*>(a.c) + bidx * a.scb,
+                           a.scm, a.m, a.n, m0 + wm * 64, n0 + wn * 128, lane, value);
+      return;
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int mm = row_base + 16 * i;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int nn = col_base + 16 * j;
+        float v[4];
+        value(i, j, v);
+        if (mm >= a.m || nn >= a.n) continue;
+        __bf16* p = reinterpret_cast<__bf16*>(a.c) + bidx * a.scb + int64_t(mm) * a.scm + nn;
+        if (plain && nn + 4 <= a.n && (reinterpret_cast<uintptr_t>(p) & 7) == 0) {
+          *reinterpret_cast<uint2*>(p) = make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
+        } else {
+          epilogue_general(a.c, bidx * a.scb + int64_t(mm) * a.scm, a.c_dtype, a.bias,
+                           bidx * a.sbiasb + int64_t(mm) * a.sbiasm, a.sbiasn, a.bias_dtype, a.act, nn,
+                           min(4, a.n - nn), v[0], v[1], v[2], v[3]);
+        }
+      }
     }
   };
-  if (staged_output_ok(a.c, a.scb, a.scm, a.n, plain)) {
-    // the stage the last K step did not read is free (every wave passed the
-    // last barrier after its final read of it): 8 KiB of it per wave
-    store_subtile_staged(smem + (ksteps & 1) * STAGE + wave * 8192, reinterpret_cast<__bf16*>(a.c) + bidx * a.scb,
-                         a.scm, a.m, a.n, m0 + wm * 64, n0 + wn * 128, lane, value);
-    return;
-  }
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int mm = row_base + 16 * i;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int nn = col_base + 16 * j;
-      float v[4];
-      value(i, j, v);
-      if (mm >= a.m || nn >= a.n) continue;
-      __bf16* p = reinterpret_cast<__bf16*>(a.c) + bidx * a.scb + int64_t(mm) * a.scm + nn;
-      if (plain && nn + 4 <= a.n && (reinterpret_cast<uintptr_t>(p) & 7) == 0) {
-        *reinterpret_cast<uint2*>(p) = make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
-      } else {
-        epilogue_general(a.c, bidx * a.scb + int64_t(mm) * a.scm, a.c_dtype, a.bias,
-                         bidx * a.sbiasb + int64_t(mm) * a.sbiasm, a.sbiasn, a.bias_dtype, a.act, nn,
-                         min(4, a.n - nn), v[0], v[1], v[2], v[3]);
-      }
-    }
+  if constexpr (MODE == 1) {
+    if (a.scales_are_quant) epilogue(std::true_type{});
+    else epilogue(std::false_type{});
+  } else {
+    epilogue(std::false_type{});
   }
 }
 
@@ -543,64 +555,75 @@ __global__ __launch_bounds__(NT, STAGED ? 3 : 2) void bmm_single_kernel(FastArgs
   v8i af[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) af[i] = frag(smem, wm * 64 + i * 16 + lr, lg);
-  float tscale = 1.0f;
-  if constexpr (MODE == 2) tscale = a.scales_are_quant ? 1.0f / (a.sa[0] * a.sb[0]) : a.sa[0];
-  const bool plain = a.bias == nullptr && a.act == PCAMD_ACT_NONE && a.c_dtype == kBF16;
-  if constexpr (STAGED) {
-    // every wave holds its A fragments: the A region becomes the staging area
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-    __syncthreads();
-  }
-  // The wave's 64 x 128 output in two 64 x 64 halves, so only 64
-  // accumulators are live and three workgroups fit on a CU.
-#pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    v4f acc[4][4];
-#pragma unroll
-    for (int jj = 0; jj < 4; ++jj) {
-      v8i bf;
-      if constexpr (B_K) bf = frag(smem + A_BYTES, wn * 128 + (4 * h + jj) * 16 + lr, lg);
-      else bf = lds::frag_mn<BN>(smem + A_BYTES, wn * 128 + (4 * h + jj) * 16, lane);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) acc[i][jj] = mfma<FMT>(bf, af[i], v4f{0.f, 0.f, 0.f, 0.f});
-    }
-    auto value = [&](int i, int jj, float (&v)[4]) {
-      const int j = 4 * h + jj;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        float s;
-        if constexpr (MODE == 0) s = sav[i] * sbv[j][SB_COL ? r : 0];  // (sa * sb), then * P
-        else if constexpr (MODE == 1) {
-          s = sav[i] * sbv[j][r];
-          if (a.scales_are_quant) s = 1.0f / s;
-        } else s = tscale;
-        v[r] = acc[i][jj][r] * s;
-      }
-    };
+  // SAQ (scales_are_quant, channel mode): 1 / (sa * sb) per element, a
+  // compile-time branch so that the other case carries no division
+  auto epilogue = [&](auto saq_c) {
+    constexpr bool SAQ = decltype(saq_c)::value;
+    float tscale = 1.0f;
+    if constexpr (MODE == 2) tscale = a.scales_are_quant ? 1.0f / (a.sa[0] * a.sb[0]) : a.sa[0];
+    const bool plain = a.bias == nullptr && a.act == PCAMD_ACT_NONE && a.c_dtype == kBF16;
     if constexpr (STAGED) {
-      store_half_staged(smem + wave * 4096, reinterpret_cast<__bf16*>(a.c) + bidx * a.scb, a.scm, a.m, a.n,
-                        m0 + wm * 64, n0 + wn * 128 + 64 * h, lane, value);
-      continue;
+      // every wave holds its A fragments: the A region becomes the staging area
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      __syncthreads();
     }
+    // The wave's 64 x 128 output in two 64 x 64 halves, so only 64
+    // accumulators are live and three workgroups fit on a CU.
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int mm = row_base + 16 * i;
+    for (int h = 0; h < 2; ++h) {
+      v4f acc[4][4];
 #pragma unroll
       for (int jj = 0; jj < 4; ++jj) {
-        const int nn = col_base + 16 * (4 * h + jj);
-        float v[4];
-        value(i, jj, v);
-        if (mm >= a.m || nn >= a.n) continue;
-        __bf16* p = reinterpret_cast<__bf16*>(a.c) + bidx * a.scb + int64_t(mm) * a.scm + nn;
-        if (plain && nn + 4 <= a.n && (reinterpret_cast<uintptr_t>(p) & 7) == 0) {
-          *reinterpret_cast<uint2*>(p) = make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
-        } else {
-          epilogue_general(a.c, bidx * a.scb + int64_t(mm) * a.scm, a.c_dtype, a.bias,
-                           bidx * a.sbiasb + int64_t(mm) * a.sbiasm, a.sbiasn, a.bias_dtype, a.act, nn,
-                           min(4, a.n - nn), v[0], v[1], v[2], v[3]);
+        v8i bf;
+        if constexpr (B_K) bf = frag(smem + A_BYTES, wn * 128 + (4 * h + jj) * 16 + lr, lg);
+        else bf = lds::frag_mn<BN>(smem + A_BYTES, wn * 128 + (4 * h + jj) * 16, lane);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[i][jj] = mfma<FMT>(bf, af[i], v4f{0.f, 0.f, 0.f, 0.f});
+      }
+      auto value = [&](int i, int jj, float (&v)[4]) {
+        const int j = 4 * h + jj;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          float s;
+          if constexpr (MODE == 0) s = sav[i] * sbv[j][SB_COL ? r : 0];  // (sa * sb), then * P
+          else if constexpr (MODE == 1) {
+            s = sav[i] * sbv[j][r];
+            if constexpr (SAQ) s = 1.0f / s;
+          } else s = tscale;
+          v[r] = acc[i][jj][r] * s;
+        }
+      };
+      if constexpr (STAGED) {
+        store_half_staged(smem + wave * 4096, reinterpret_cast<__bf16*>(a.c) + bidx * a.scb, a.scm, a.m, a.n,
+                          m0 + wm * 64, n0 + wn * 128 + 64 * h, lane, value);
+        continue;
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int mm = row_base + 16 * i;
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) {
+          const int nn = col_base + 16 * (4 * h + jj);
+          float v[4];
+          value(i, jj, v);
+          if (mm >= a.m || nn >= a.n) continue;
+          __bf16* p = reinterpret_cast<__bf16*>(a.c) + bidx * a.scb + int64_t(mm) * a.scm + nn;
+          if (plain && nn + 4 <= a.n && (reinterpret_cast<uintptr_t>(p) & 7) == 0) {
+            *reinterpret_cast<uint2*>(p) = make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
+          } else {
+            epilogue_general(a.c, bidx * a.scb + int64_t(mm) * a.scm, a.c_dtype, a.bias,
+                             bidx * a.sbiasb + int64_t(mm) * a.sbiasm, a.sbiasn, a.bias_dtype, a.act, nn,
+                             min(4, a.n - nn), v[0], v[1], v[2], v[3]);
+          }
         }
       }
     }
+  };
+  if constexpr (MODE == 1) {
+    if (a.scales_are_quant) epilogue(std::true_type{});
+    else epilogue(std::false_type{});
+  } else {
+    epilogue(std::false_type{});
   }
 }
 

@@ -500,82 +500,95 @@ __global__ __launch_bounds__(NT, 1) void bmm_wide_kernel(FastArgs a) {
   const int col_base = n0 + wcol + 4 * lg;
 
   // ---- epilogue ----
-  float tscale = 1.0f;
-  if constexpr (MODE == 2) tscale = a.scales_are_quant ? 1.0f / (a.sa[0] * a.sb[0]) : a.sa[0];
-  // output value (i, j, r) of this lane with the channel / tensor scales applied
-  // column scales of sub-tile column j (channel mode; 1 otherwise)
-  auto col_scales = [&](int j, float (&sbv)[4]) {
+  // SAQ (scales_are_quant, channel mode): the per-element scale is
+  // 1 / (sa * sb). It is a compile-time branch of the epilogue: as a runtime
+  // condition inside the unrolled element loops it was if-converted, and
+  // every output paid for a division it did not use.
+  auto epilogue = [&](auto saq_c) {
+    constexpr bool SAQ = decltype(saq_c)::value;
+    float tscale = 1.0f;
+    if constexpr (MODE == 2) tscale = a.scales_are_quant ? 1.0f / (a.sa[0] * a.sb[0]) : a.sa[0];
+    // output value (i, j, r) of this lane with the channel / tensor scales applied
+    // column scales of sub-tile column j (channel mode; 1 otherwise)
+    auto col_scales = [&](int j, float (&sbv)[4]) {
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      sbv[r] = 1.0f;
-      if constexpr (MODE == 1) {
-        const int nn = col_base + 16 * j + r;
-        sbv[r] = nn < a.n ? a.sb[bidx * a.ssbb + int64_t(nn) * a.ssb1] : 0.0f;
+      for (int r = 0; r < 4; ++r) {
+        sbv[r] = 1.0f;
+        if constexpr (MODE == 1) {
+          const int nn = col_base + 16 * j + r;
+          sbv[r] = nn < a.n ? a.sb[bidx * a.ssbb + int64_t(nn) * a.ssb1] : 0.0f;
+        }
       }
-    }
-  };
-  auto out_value = [&](int i, int j, int r, float sam_v, const float (&sbv)[4]) -> float {
-    float x = acc[i][j][r];
-    if constexpr (MODE == 1) {
-      float s = sam_v * sbv[r];
-      if (a.scales_are_quant) s = 1.0f / s;
-      x *= s;
-    } else if constexpr (MODE == 2) {
-      x *= tscale;
-    }
-    return x;
-  };
-  auto row_scale = [&](int i) -> float {
-    float sam_v = 1.0f;
-    if constexpr (MODE == 1) {
-      const int mm = row_base + 16 * i;
-      sam_v = mm < a.m ? a.sa[bidx * a.ssab + int64_t(mm) * a.ssa1] : 0.0f;
-    }
-    return sam_v;
-  };
-  const bool plain = a.bias == nullptr && a.act == PCAMD_ACT_NONE && a.c_dtype == kBF16;
-  if (staged_output_ok(a.c, a.scb, a.scm, a.n, plain)) {
-    // each wave stages its sub-tile in 8 KiB (4 KiB for a half tile) of the
-    // LDS stage the last K step did not read (no other wave touches it, so no
-    // barrier is needed)
-    const float sam_v[4] = {row_scale(0), row_scale(1), row_scale(2), row_scale(3)};
-    auto value = [&](int i, int j, float (&v)[4]) {
-      float sbv[4];
-      col_scales(j, sbv);
-#pragma unroll
-      for (int r = 0; r < 4; ++r) v[r] = out_value(i, j, r, sam_v[i], sbv);
     };
-    __bf16* cb = reinterpret_cast<__bf16*>(a.c) + bidx * a.scb;
-    if constexpr (JN == 8)
-      store_subtile_staged(smem + (ksteps & 1) * STAGE + wave * 8192, cb, a.scm, a.m, a.n, m0 + wm * 64,
-                           n0 + wcol, lane, value);
-    else
-      store_half_staged(smem + (ksteps & 1) * STAGE + wave * 4096, cb, a.scm, a.m, a.n, m0 + wm * 64, n0 + wcol,
-                        lane, value);
-    return;
-  }
+    auto out_value = [&](int i, int j, int r, float sam_v, const float (&sbv)[4]) -> float {
+      float x = acc[i][j][r];
+      if constexpr (MODE == 1) {
+        float s = sam_v * sbv[r];
+        if constexpr (SAQ) s = 1.0f / s;
+        x *= s;
+      } else if constexpr (MODE == 2) {
+        x *= tscale;
+      }
+      return x;
+    };
+    auto row_scale = [&](int i) -> float {
+      float sam_v = 1.0f;
+      if constexpr (MODE == 1) {
+        const int mm = row_base + 16 * i;
+        sam_v = mm < a.m ? a.sa[bidx * a.ssab + int64_t(mm) * a.ssa1] : 0.0f;
+      }
+      return sam_v;
+    };
+    const bool plain = a.bias == nullptr && a.act == PCAMD_ACT_NONE && a.c_dtype == kBF16;
+    if (staged_output_ok(a.c, a.scb, a.scm, a.n, plain)) {
+      // each wave stages its sub-tile in 8 KiB (4 KiB for a half tile) of the
+      // LDS stage the last K step did not read (no other wave touches it, so no
+      // barrier is needed)
+      const float sam_v[4] = {row_scale(0), row_scale(1), row_scale(2), row_scale(3)};
+      auto value = [&](int i, int j, float (&v)[4]) {
+        float sbv[4];
+        col_scales(j, sbv);
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int mm = row_base + 16 * i;
-    const float sam_v = row_scale(i);
+        for (int r = 0; r < 4; ++r) v[r] = out_value(i, j, r, sam_v[i], sbv);
+      };
+      __bf16* cb = reinterpret_cast<__bf16*>(a.c) + bidx * a.scb;
+      if constexpr (JN == 8)
+        store_subtile_staged(smem + (ksteps & 1) * STAGE + wave * 8192, cb, a.scm, a.m, a.n, m0 + wm * 64,
+                             n0 + wcol, lane, value);
+      else
+        store_half_staged(smem + (ksteps & 1) * STAGE + wave * 4096, cb, a.scm, a.m, a.n, m0 + wm * 64, n0 + wcol,
+                          lane, value);
+      return;
+    }
 #pragma unroll
-    for (int j = 0; j < JN; ++j) {
-      const int nn = col_base + 16 * j;
-      float sbv[4];
-      col_scales(j, sbv);
-      float v[4];
+    for (int i = 0; i < 4; ++i) {
+      const int mm = row_base + 16 * i;
+      const float sam_v = row_scale(i);
 #pragma unroll
-      for (int r = 0; r < 4; ++r) v[r] = out_value(i, j, r, sam_v, sbv);
-      if (mm >= a.m || nn >= a.n) continue;
-      __bf16* p = reinterpret_cast<__bf16*>(a.c) + bidx * a.scb + int64_t(mm) * a.scm + nn;
-      if (plain && nn + 4 <= a.n && (reinterpret_cast<uintptr_t>(p) & 7) == 0) {
-        *reinterpret_cast<uint2*>(p) = make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
-      } else {
-        epilogue_general(a.c, bidx * a.scb + int64_t(mm) * a.scm, a.c_dtype, a.bias,
-                         bidx * a.sbiasb + int64_t(mm) * a.sbiasm, a.sbiasn, a.bias_dtype, a.act, nn,
-                         min(4, a.n - nn), v[0], v[1], v[2], v[3]);
+      for (int j = 0; j < JN; ++j) {
+        const int nn = col_base + 16 * j;
+        float sbv[4];
+        col_scales(j, sbv);
+        float v[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) v[r] = out_value(i, j, r, sam_v, sbv);
+        if (mm >= a.m || nn >= a.n) continue;
+        __bf16* p = reinterpret_cast<__bf16*>(a.c) + bidx * a.scb + int64_t(mm) * a.scm + nn;
+        if (plain && nn + 4 <= a.n && (reinterpret_cast<uintptr_t>(p) & 7) == 0) {
+          *reinterpret_cast<uint2*>(p) = make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
+        } else {
+          epilogue_general(a.c, bidx * a.scb + int64_t(mm) * a.scm, a.c_dtype, a.bias,
+                           bidx * a.sbiasb + int64_t(mm) * a.sbiasm, a.sbiasn, a.bias_dtype, a.act, nn,
+                           min(4, a.n - nn), v[0], v[1], v[2], v[3]);
+        }
       }
     }
+  };
+  if constexpr (MODE == 1) {
+    if (a.scales_are_quant) epilogue(std::true_type{});
+    else epilogue(std::false_type{});
+  } else {
+    epilogue(std::false_type{});
   }
 }
 

@@ -138,7 +138,7 @@ def _quant_scales(shape, seed):
 def _bmm_abi(a, b, c, sa, sb, mode, saq):
     rc = _lib.lib().pcamd_bmm_scaled(
         _lib.ptr(a), _lib.ptr(b), _lib.E4M3FN, a.shape[0], a.shape[1], b.shape[2], a.shape[2],
-        *a.stride(), *b.stride(), _lib.ptr(c), _lib.F32, *c.stride(), None, 0, 0, 0, 0,
+        *a.stride(), *b.stride(), _lib.ptr(c), _lib.dtype_code(c.dtype), *c.stride(), None, 0, 0, 0, 0,
         _lib.ptr(sa), *(sa.stride() + (0,) * (3 - sa.dim())), _lib.ptr(sb),
         *(sb.stride() + (0,) * (3 - sb.dim())), mode, saq, 1, 128, 1, _lib.ACT_NONE, _lib.stream_of(c))
     _lib.check(rc, "pcamd_bmm_scaled")
@@ -151,11 +151,16 @@ KERNEL_SHAPES = {"single_k128": (2, 256, 384, 128), "wide_k512": (2, 512, 512, 5
                  "general_unaligned": (2, 33, 47, 200)}
 
 
+@pytest.mark.parametrize("out", ["f32", "bf16"])
 @pytest.mark.parametrize("mode", ["channel", "tensor"])
 @pytest.mark.parametrize("kernel", sorted(KERNEL_SHAPES))
-def test_scales_are_quant(dev, kernel, mode):
+def test_scales_are_quant(dev, kernel, mode, out):
+    """fp32 output goes through the per-element epilogue, bf16 output (aligned
+    shapes) through the LDS-staged one of the single-step and wide kernels."""
     bsz, m, n, k = KERNEL_SHAPES[kernel]
-    print(f"scales_are_quant {kernel} {mode}", flush=True)
+    print(f"scales_are_quant {kernel} {mode} {out}", flush=True)
+    odt = torch.float32 if out == "f32" else torch.bfloat16
+    tol = 1e-4 if out == "f32" else 1e-2  # fp32: accumulation order and the scale rounding; bf16: its rounding
     a, b = _fp8((bsz, m, k), 1), _fp8((bsz, k, n), 2)
     if mode == "channel":
         qsa, qsb = _quant_scales((bsz, m), 3), _quant_scales((bsz, n), 4)
@@ -169,14 +174,14 @@ def test_scales_are_quant(dev, kernel, mode):
                      O.decode(b.view(torch.uint8).numpy()).astype(np.float64))
     ref = prod * factor.numpy()
     ad, bd = a.to(dev), b.to(dev)
-    c = torch.empty(bsz, m, n, dtype=torch.float32, device=dev)
+    c = torch.empty(bsz, m, n, dtype=odt, device=dev)
     _bmm_abi(ad, bd, c, qsa.to(dev), qsb.to(dev), code, 1)
-    err = O.max_abs_rel(c.cpu().numpy(), ref)
-    assert err <= 1e-4, err  # fp32 output: only accumulation order and the scale rounding differ
+    err = O.max_abs_rel(c.float().cpu().numpy(), ref)
+    assert err <= tol, err
     # the same product through dequant scales (scales_are_quant = 0)
     c0 = torch.empty_like(c)
     if mode == "channel":
         _bmm_abi(ad, bd, c0, (1.0 / qsa).to(dev), (1.0 / qsb).to(dev), code, 0)
     else:
         _bmm_abi(ad, bd, c0, (1.0 / (qsa * qsb)).to(dev), qsb.to(dev), code, 0)
-    assert O.max_abs_rel(c0.cpu().numpy(), ref) <= 1e-4
+    assert O.max_abs_rel(c0.float().cpu().numpy(), ref) <= tol
