@@ -21,6 +21,7 @@ from __future__ import annotations
 
 import argparse
 import json
+import math
 import os
 import statistics
 import sys
@@ -74,6 +75,9 @@ def parse():
     p.add_argument("--pmc-probe", action="store_true",
                    help="eager launches for rocprofv3 --pmc passes: 3 plain bf16 copies of "
                         "256 MiB (calibration) then 3 config-2 quantizations")
+    p.add_argument("--mem-ceiling", action="store_true",
+                   help="graph-timed torch copy / conversion / fill kernels with the traffic mixes of the "
+                        "workloads (one JSON line): what plain memory-bound kernels reach on this GPU")
     p.add_argument("--gemm-ref", choices=["graph", "eager"], default=None,
                    help="the config-5 GEMM shapes with tensor and row/column scales, this build's kernels "
                         "next to hipBLASLt (torch._scaled_mm): 'graph' times them (HIP graphs, one JSON "
@@ -703,6 +707,32 @@ def pmc_probe_bmm(torch, dev):
                       "order": ["copy x3", "config4 x3"] + [f"{k} x3" for k in gemms]}))
 
 
+def mem_ceiling(torch, dev, steps, warmup):
+    """What plain memory-bound kernels (PyTorch's own elementwise kernels)
+    reach for the read:write mixes of this build's workloads, graph-timed
+    like the workloads over rotating buffers beyond the 256 MB MALL:
+    - 2:1 (the quantizers): bf16 -> fp8 conversion of [18432, 7168] (config 2's shape);
+    - 1:1 (the dual quantizer): bf16 copy of [8192, 14336] (config 5's dY);
+    - 0:1 (config 4's output, 268 MB of its 311 MB): bf16 fill of [128, 2048, 512]."""
+    res = {}
+    cases = {
+        "convert_bf16_to_fp8_18432x7168": ((18432, 7168), lambda src, dst: dst.copy_(src), torch.float8_e4m3fn, 3),
+        "copy_bf16_8192x14336": ((8192, 14336), lambda src, dst: dst.copy_(src), torch.bfloat16, 4),
+        "fill_bf16_128x2048x512": ((128, 2048, 512), lambda src, dst: dst.zero_(), torch.bfloat16, 2),
+    }
+    for name, (shape, op, odt, bpe) in cases.items():
+        nsets = 4
+        srcs = [torch.randn(*shape, device=dev).bfloat16() for _ in range(nsets)] if bpe != 2 else [None] * nsets
+        dsts = [torch.empty(*shape, dtype=odt, device=dev) for _ in range(nsets)]
+        ms, _ = graph_time(torch, lambda i: op(srcs[i % nsets], dsts[i % nsets]), steps, warmup, settle_ms=SETTLE_MS)
+        nbytes = math.prod(shape) * bpe
+        res[name] = {"ms": ms, "bytes": nbytes, "GB/s": nbytes / (ms * 1e-3) / 1e9,
+                     "frac_of_hbm_peak": nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS}
+        del srcs, dsts
+        torch.cuda.empty_cache()
+    print(json.dumps({"mem_ceiling": res}))
+
+
 def gemm_ref(torch, dev, steps, warmup, eager):
     """Reference point for the config-5 GEMMs: the same three products with
     per-tensor scales and the forward with row / column scales, run by this
@@ -793,6 +823,9 @@ def main():
         return
     if args.pmc_probe_bmm:
         pmc_probe_bmm(torch, dev)
+        return
+    if args.mem_ceiling:
+        mem_ceiling(torch, dev, args.steps, args.warmup)
         return
     if args.gemm_ref:
         gemm_ref(torch, dev, args.steps, args.warmup, args.gemm_ref == "eager")
