@@ -321,6 +321,16 @@ __global__ __launch_bounds__(NT, 1) void bmm_wide_kernel(FastArgs a) {
   // prologue: step 0 resident in stage 0 (step 0's sub-tiles start step 1's DMA)
   issue(0, smem);
   if constexpr (MODE == 0) store_scale(0, load_scale(0));
+  if constexpr (MODE == 1) {
+    // channel scales of the tile's 256 rows (waves 0-3) and 256 columns
+    // (waves 4-7), read by the epilogue from LDS; 0 past the matrix, where
+    // no output is stored
+    const int idx = (row_scales ? m0 : n0) + slot;
+    const bool in = idx < (row_scales ? a.m : a.n);
+    const float* sp = row_scales ? a.sa + bidx * a.ssab + int64_t(min(idx, a.m - 1)) * a.ssa1
+                                 : a.sb + bidx * a.ssbb + int64_t(min(idx, a.n - 1)) * a.ssb1;
+    (row_scales ? sa_tile : sb_tile)[slot] = in ? *sp : 0.0f;
+  }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
   float sc_next = 0.0f;
@@ -514,10 +524,7 @@ __global__ __launch_bounds__(NT, 1) void bmm_wide_kernel(FastArgs a) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         sbv[r] = 1.0f;
-        if constexpr (MODE == 1) {
-          const int nn = col_base + 16 * j + r;
-          sbv[r] = nn < a.n ? a.sb[bidx * a.ssbb + int64_t(nn) * a.ssb1] : 0.0f;
-        }
+        if constexpr (MODE == 1) sbv[r] = sb_tile[wcol + 4 * lg + 16 * j + r];
       }
     };
     auto out_value = [&](int i, int j, int r, float sam_v, const float (&sbv)[4]) -> float {
@@ -533,10 +540,7 @@ __global__ __launch_bounds__(NT, 1) void bmm_wide_kernel(FastArgs a) {
     };
     auto row_scale = [&](int i) -> float {
       float sam_v = 1.0f;
-      if constexpr (MODE == 1) {
-        const int mm = row_base + 16 * i;
-        sam_v = mm < a.m ? a.sa[bidx * a.ssab + int64_t(mm) * a.ssa1] : 0.0f;
-      }
+      if constexpr (MODE == 1) sam_v = sa_tile[wm * 64 + 16 * i + lr];
       return sam_v;
     };
     const bool plain = a.bias == nullptr && a.act == PCAMD_ACT_NONE && a.c_dtype == kBF16;
