@@ -331,7 +331,12 @@ __global__ __launch_bounds__(NT, 1) void bmm_wide_kernel(FastArgs a) {
                                  : a.sb + bidx * a.ssbb + int64_t(min(idx, a.n - 1)) * a.ssb1;
     (row_scales ? sa_tile : sb_tile)[slot] = in ? *sp : 0.0f;
   }
+  // tensor scale: loaded here, under the first K step's DMA, rather than
+  // after the K loop where the epilogue would wait for it
+  float tscale = 1.0f;
+  if constexpr (MODE == 2) tscale = a.scales_are_quant ? 1.0f / (a.sa[0] * a.sb[0]) : a.sa[0];
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  if constexpr (MODE == 2) asm volatile("" : "+v"(tscale));  // materialised before the K loop
   __syncthreads();
   float sc_next = 0.0f;
   if constexpr (MODE == 0) sc_next = load_scale(1);
@@ -516,8 +521,6 @@ __global__ __launch_bounds__(NT, 1) void bmm_wide_kernel(FastArgs a) {
   // every output paid for a division it did not use.
   auto epilogue = [&](auto saq_c) {
     constexpr bool SAQ = decltype(saq_c)::value;
-    float tscale = 1.0f;
-    if constexpr (MODE == 2) tscale = a.scales_are_quant ? 1.0f / (a.sa[0] * a.sb[0]) : a.sa[0];
     // output value (i, j, r) of this lane with the channel / tensor scales applied
     // column scales of sub-tile column j (channel mode; 1 otherwise)
     auto col_scales = [&](int j, float (&sbv)[4]) {
