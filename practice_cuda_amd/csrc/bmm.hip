@@ -232,9 +232,11 @@ __device__ __attribute__((noinline)) void epilogue_general(const Args& a, int64_
   }
 }
 
+// Two floats to bf16 (round to nearest even) as one v_cvt_pk_bf16_f32.
 PCAMD_DEV uint32_t pack_bf16x2(float lo, float hi) {
-  return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<__bf16>(lo))) |
-         (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<__bf16>(hi))) << 16);
+  typedef float f32x2 __attribute__((ext_vector_type(2)));
+  typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{lo, hi}, bf16x2));
 }
 
 template <bool A_K, bool B_K, int FMT, int MODE>

@@ -16,9 +16,13 @@
 
 namespace pcamd {
 
+// Two floats to bf16 (round to nearest even), lo in the low half. Converted
+// as a pair so that it is one v_cvt_pk_bf16_f32; converting each float on
+// its own costs two of them plus a shift and an OR.
 PCAMD_DEV uint32_t pack_bf16_pair(float lo, float hi) {
-  return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<__bf16>(lo))) |
-         (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<__bf16>(hi))) << 16);
+  typedef float f32x2 __attribute__((ext_vector_type(2)));
+  typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{lo, hi}, bf16x2));
 }
 
 // Whether the staged path applies: bf16 output without bias or activation,
