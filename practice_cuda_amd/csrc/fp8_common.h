@@ -71,6 +71,14 @@ PCAMD_DEV void load_chunk(Chunk<DT>& c, const void* p) {
   }
 }
 
+// The same with ordinary loads, for input that is read again soon.
+template <int DT>
+PCAMD_DEV void load_chunk_temporal(Chunk<DT>& c, const void* p) {
+  const uint4* q = static_cast<const uint4*>(p);
+  c.r[0] = q[0];
+  if constexpr (DT == kF32) c.r[1] = q[1];
+}
+
 template <int DT>
 PCAMD_DEV void zero_chunk(Chunk<DT>& c) {
   c.r[0] = make_uint4(0, 0, 0, 0);

@@ -736,7 +736,10 @@ __global__ __launch_bounds__(kThreads) void colchan_zero_kernel(ColArgs a) {
 // columns 8 (t % 16) .. + 7 of rows t / 16 + 16 p (p < 8) of its slab. The
 // slab's column maxima (lane shuffles, then LDS across the waves) go to the
 // scale slots by atomic max on the fp32 bit patterns (for non-negative
-// values their uint32 order is the float order).
+// values their uint32 order is the float order). The input is read with
+// ordinary (temporal) loads, unlike the other kernels: the apply kernel
+// reads it again right after, and what the caches keep of it saves HBM
+// reads ([18432, 7168] bf16: 117 -> 106 us for the pair).
 template <int DT>
 __global__ __launch_bounds__(kThreads) void colchan_amax_kernel(ColArgs a) {
   constexpr int EB = elem_bytes<DT>();
@@ -752,7 +755,7 @@ __global__ __launch_bounds__(kThreads) void colchan_amax_kernel(ColArgs a) {
 #pragma unroll
   for (int p = 0; p < CPT; ++p) {
     const int64_t r = r0 + p * 16 + rs;
-    if (r < a.m && col < a.n) load_chunk<DT>(raw[p], xb + (r * a.sxm + col) * EB);
+    if (r < a.m && col < a.n) load_chunk_temporal<DT>(raw[p], xb + (r * a.sxm + col) * EB);
     else zero_chunk<DT>(raw[p]);
   }
   float cmax[8] = {0, 0, 0, 0, 0, 0, 0, 0};
