@@ -146,7 +146,6 @@ def make_config2(torch):
 
 
 def make_config3(torch):
-    import math
     g = torch.Generator().manual_seed(0)
     w = torch.randn(4096, 7168, generator=g) * 0.02
     mult = torch.exp(torch.empty(32, 56).uniform_(math.log(0.1), math.log(10.0), generator=g))
@@ -757,7 +756,7 @@ def gemm_ref(torch, dev, steps, warmup, eager):
     bf = torch.bfloat16
     sx, sw, sdy = (r.dequant_scale.reshape(()).float() for r in (tx, tw, tdy))
     x8, w8, dy8 = tx.tensor[0], tw.tensor[0], tdy.tensor[0]
-    w_cm = w8.t().contiguous().t()               # [N, K] column-major
+    w_cm = w8.t().contiguous().t()               # [N, K] column-major: dgrad's B contiguous along N
     dyt8 = dy8.t().contiguous()                  # [N, M] row-major
     x_cm = x8.t().contiguous().t()               # [M, K] column-major
     out_f = torch.empty(1, M, N, dtype=bf, device=dev)
@@ -773,7 +772,7 @@ def gemm_ref(torch, dev, steps, warmup, eager):
     cases = {
         "tensor_fwd": (lambda i: hip_per_tensor_bmm(tx, view(tw, tw.tensor.transpose(-1, -2)), out=out_f),
                        lambda i: torch._scaled_mm(x8, w8.t(), scale_a=sx, scale_b=sw, out_dtype=bf)),
-        "tensor_dgrad": (lambda i: hip_per_tensor_bmm(tdy, tw, out=out_d),
+        "tensor_dgrad": (lambda i: hip_per_tensor_bmm(tdy, view(tw, w_cm[None]), out=out_d),
                          lambda i: torch._scaled_mm(dy8, w_cm, scale_a=sdy, scale_b=sw, out_dtype=bf)),
         "tensor_wgrad": (lambda i: hip_per_tensor_bmm(a_w, b_w, out=out_w),
                          lambda i: torch._scaled_mm(dyt8, x_cm, scale_a=sdy, scale_b=sx, out_dtype=bf)),
@@ -802,7 +801,8 @@ def gemm_ref(torch, dev, steps, warmup, eager):
         res[name] = row
     if not eager:
         print(json.dumps({"gemm_ref": res, "shape": {"M": M, "K": K, "N": N},
-                          "note": "fwd X W^T, dgrad dY W, wgrad dY^T X on K-major operands"}))
+                          "note": "fwd X W^T, dgrad dY W, wgrad dY^T X; both sides get the same operand "
+                                  "layouts, contiguous along the reduction (what torch._scaled_mm takes)"}))
 
 
 def main():
