@@ -61,6 +61,20 @@ def test_quant_e5m2_format_enum(dev):
     assert np.array_equal(q.view(torch.uint8).cpu().numpy(), q_ref)
 
 
+@pytest.mark.parametrize("dtype,quant_dtype,fmt,fp8_range", [
+    (torch.bfloat16, torch.float8_e4m3fn, "e4m3", 240.0),
+    (torch.float16, torch.float8_e4m3fn, "e4m3", 100.0),
+    (torch.float32, torch.float8_e4m3fn, "e4m3", float(np.nextafter(np.float32(248.0), np.float32(0.0)))),
+    (torch.bfloat16, torch.float8_e5m2, "e5m2", 36864.0),
+])
+def test_quant_fp8_range_argument(dev, dtype, quant_dtype, fmt, fp8_range):
+    """A caller-chosen fp8_range (fp8_warper.py:12) below the format maximum:
+    the clamping kernel and the scale arithmetic in the input's dtype, bit for
+    bit against the oracle."""
+    print(f"legacy fp8_range={fp8_range} {dtype} {fmt}", flush=True)
+    _check_quant(_randn((3, 100, 300), 9, dtype, 2.0), dev, fmt, quant_dtype, fp8_range)
+
+
 def test_quant_reference_name_alias(dev):
     assert fp8_quant_triton is fp8_quant
     x = _randn((32, 64), 4)
