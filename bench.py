@@ -729,6 +729,14 @@ def mem_ceiling(torch, dev, steps, warmup):
                      "frac_of_hbm_peak": nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS}
         del srcs, dsts
         torch.cuda.empty_cache()
+    # per-launch floor: the 1x128 quantizer on one row, back to back in a graph
+    from practice_cuda_amd import _lib as L
+    tiny = torch.randn(1, 7168, device=dev).bfloat16()
+    ty = torch.empty(1, 7168, dtype=torch.float8_e4m3fn, device=dev)
+    ts = torch.empty(1, 56, device=dev)
+    launch = quant_block_launcher(torch, L, [tiny], [ty], [ts], 1, 128)
+    ms, _ = graph_time(torch, launch, steps, warmup)
+    res["launch_floor_1x128_one_row"] = {"ms": ms, "note": "one workgroup; the fixed cost of one launch in a graph"}
     print(json.dumps({"mem_ceiling": res}))
 
 
