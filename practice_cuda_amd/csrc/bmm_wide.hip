@@ -12,16 +12,16 @@
 // 256 x 128 halves, two workgroups per tile, each wave computing 64 x 64
 // (JN = 4 sub-tiles instead of 8). A half loads the whole tile's operands -
 // the loaders and LDS layout are the same - and reads the B fragments of its
-// own 128 columns. The last wave then takes about half a tile's time.
+// own 128 columns, so it takes more than half of a whole tile's time.
 //
 // Both operands go global -> LDS with buffer_load_dwordx4 ... lds (no VGPR
 // staging), one K step ahead of the MFMAs. The LDS layout follows the global
 // one:
 //   K-major operand (rows contiguous along k): [row][8 x 16 B], chunk c of
-//     row r at position c ^ ((r ^ r >> 4) & 7); fragments are two
+//     row r at position c ^ swz_k(r) (below); fragments are two
 //     ds_read_b128 per lane.
 //   MN-major operand (k rows contiguous along m / n): [k][16 x 16 B], chunk c
-//     of k-row k at position c ^ (k & 7); fragments are four
+//     of k-row k at position c ^ swz_mn(k) (bmm_lds.h); fragments are four
 //     ds_read_b64_tr_b8 per lane. Within a 16-lane group, lane j addresses
 //     8 bytes of k-row (k0 + j / 2) at column (col0 + 8 (j & 1)), and lane c
 //     receives column (col0 + c) of those eight k-rows, i.e. 8 consecutive k
@@ -32,7 +32,8 @@
 // Scales: block mode (quant_block_k == 128) folds each step's partial,
 // acc += P * (sa * sb) (xuOAO/practice_cuda kernels/bmm/per_block.py:99-111),
 // with the step's scales staged in LDS; channel / tensor scales are applied
-// once in the epilogue. Wider quant-K blocks use bmm_fast.hip.
+// once in the epilogue (the tile's channel scales are staged in LDS in the
+// prologue). Wider quant-K blocks use bmm_fast.hip.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
