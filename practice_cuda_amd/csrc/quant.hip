@@ -1,6 +1,7 @@
 // quant.hip - gfx950 FP8 quantizers behind the C ABI (include/pcamd_fp8.h).
 //
-// Kernels (all HBM-bound; each element is read once from HBM). The streaming
+// Kernels (all HBM-bound; each element is read once, except on the per-tensor
+// and whole-column paths, whose amax pass reads it first). The streaming
 // kernels are non-persistent: one wave (or workgroup) per unit, all of its
 // loads issued up front. Measured on MI355X this streams faster than
 // persistent grids that prefetch the next unit in registers (the hardware
@@ -25,7 +26,9 @@
 //                       row maxima by DPP, column maxima as above.
 //   colchan_*_kernel    whole columns of tall tensors (channel_axis = -1):
 //                       column maxima of 128-row slabs by atomic max into
-//                       the scale slots, then a quantize pass per slab.
+//                       the scale slots (temporal loads, so the next pass
+//                       finds part of the tensor in cache), then a quantize
+//                       pass per slab.
 //   quant_cols_kernel   whole columns of up to 256 rows (channel_axis = -1,
 //                       two passes over the strip), and column groups on grids
 //                       too large for the column-group kernel's 3-D grid.
