@@ -13,7 +13,9 @@
 //     reloaded only when the range crosses into the next batch;
 //   - the next unit's A rows (16 KiB) and row scales are loaded straight into
 //     the other LDS stage while the current unit computes and stores, so
-//     after the first unit no CU waits on a load with no stores in flight.
+//     after the first unit no CU waits on a load with no stores in flight;
+//   - C leaves through LDS staging as whole 1 KiB rows, one row per store
+//     instruction.
 // Every load in the loop is an asynchronous global -> LDS copy issued from
 // inline asm, and the only compiler-visible memory operations are the C
 // stores, which nothing waits for. The loop's vmcnt waits are therefore
@@ -50,7 +52,7 @@ constexpr int B_LDS = 0;                  // B: two 256-column halves of [128 k]
 constexpr int A_LDS = UN * BK;            // 64 KiB: two stages of [128 rows][128 B]
 constexpr int SA_LDS = A_LDS + 2 * UM * BK;  // two stages of 1 KiB (128 row scales used)
 constexpr int SB_LDS = SA_LDS + 2 * 1024;    // 1 KiB: the batch's column-block scales
-constexpr int STG_LDS = SB_LDS + 1024;       // 4 KiB of output staging per wave
+constexpr int STG_LDS = SB_LDS + 1024;       // output staging: 32 rows of C (1 KiB each)
 constexpr int LDS_BYTES = STG_LDS + WAVES * 4096;
 constexpr int kStoresPerUnit = 16;        // global store instructions per wave per unit
 
@@ -137,9 +139,9 @@ __global__ __launch_bounds__(NT, 1) void bmm_stream_kernel(StreamArgs s) {
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   barrier();
 
-  uint8_t* stg = smem + STG_LDS + wave * 4096;
-  for (int u = u0; u < u1; ++u) {
-    const int st = (u - u0) & 1;
+  uint8_t* stg = smem + STG_LDS;
+  int st = 0;
+  for (int u = u0; u < u1; ++u, st ^= 1) {
     const int bidx = u / s.units_per_batch;
     const int m0 = (u - bidx * s.units_per_batch) * UM;
     const bool has_next = u + 1 < u1;
@@ -180,32 +182,38 @@ __global__ __launch_bounds__(NT, 1) void bmm_stream_kernel(StreamArgs s) {
       issue_b((u + 1) / s.units_per_batch);
     }
 
-    // epilogue: four rounds of 16 rows x 128 columns through the wave's 4 KiB
-    // of LDS (chunk c of staged row r at c ^ r), each lane then storing 16
-    // contiguous bytes: an instruction writes 4 rows x 256 bytes.
+    // epilogue: four rounds through the workgroup's 32 KiB of staging, which
+    // holds 32 whole rows of C (1 KiB each; 16-byte chunk c of staged row s
+    // at position c ^ (s & 15)). In round i, wave (wm, wn) stages rows
+    // 16 i .. 16 i + 15 of its 64 x 128 block as staged rows 16 wm + lr;
+    // after a barrier, wave w stores staged rows 4 w .. 4 w + 3, one whole
+    // 1 KiB row of C per instruction (non-temporal stores: plain ones, which
+    // keep C in L2, made config 4 12 us slower). Whole rows measured 3 us
+    // faster at config 4 than four 256-byte row pieces per instruction.
     __bf16* cb = reinterpret_cast<__bf16*>(a.c) + int64_t(bidx) * a.scb;
-    const int row0 = m0 + wm * 64, col0 = wn * 128;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         const float f = sav[i] * sbv[j];  // (sa * sb), then * P
-        const int chunk = 2 * j + (lg >> 1);
-        uint2* dst = reinterpret_cast<uint2*>(stg + lr * 256 + ((chunk ^ lr) << 4) + ((lg & 1) << 3));
+        const int chunk = wn * 16 + 2 * j + (lg >> 1);
+        uint2* dst = reinterpret_cast<uint2*>(stg + (wm * 16 + lr) * 1024 + ((chunk ^ lr) << 4) + ((lg & 1) << 3));
         *dst = make_uint2(pack_bf16_pair(acc[i][j][0] * f, acc[i][j][1] * f),
                           pack_bf16_pair(acc[i][j][2] * f, acc[i][j][3] * f));
       }
       wait_lds();
+      barrier();
 #pragma unroll
       for (int it = 0; it < 4; ++it) {
         typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
-        const int r = 4 * it + (lane >> 4);
-        const int chunk = lane & 15;
-        const u32x4 v = *reinterpret_cast<const u32x4*>(stg + r * 256 + ((chunk ^ r) << 4));
-        const int mm = row0 + 16 * i + r;
-        if (mm < a.m) __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(cb + int64_t(mm) * a.scm + col0 + 8 * chunk));
+        const int srow = 4 * wave + it;
+        const u32x4 v = *reinterpret_cast<const u32x4*>(stg + srow * 1024 + (lane << 4));
+        const int chunk = lane ^ (srow & 15);
+        const int mm = m0 + (srow >> 4) * 64 + 16 * i + (srow & 15);
+        if (mm < a.m) __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(cb + int64_t(mm) * a.scm + 8 * chunk));
       }
       wait_lds();
+      barrier();
     }
 
     if (has_next) {

@@ -9,7 +9,8 @@ bit-identical; each is also checked per batch against an fp32 bmm of the
 dequantized operands at the north_star bar (max-abs-rel <= 1e-2,
 fp8_training/fp8_bench/bench_bmm.py:414-419).
 
-Shapes cover one unit, a partial last unit, more units than CUs (each
+Shapes cover one unit, a partial last unit, fewer units than CUs with a
+partial one among them, more units than CUs (each
 workgroup walks several units and crosses batch boundaries, reloading B),
 ragged M on top of that, four B block widths and both fp8 formats.
 """
@@ -62,6 +63,7 @@ CASES = [
     (2, 2048, 16, "e4m3"),      # one B scale per 16-column sub-tile
     (2, 384, 64, "e5m2"),
     (1, 77, 512, "e4m3"),       # a single partial unit, one B scale for all columns
+    (1, 600, 128, "e4m3"),      # 5 units (one workgroup each), the last partial
     (3, 25600, 128, "e4m3"),    # 600 units: ranges of 2-3 units crossing batch boundaries
     (2, 38477, 128, "e4m3"),    # the same with a partial unit at the end of each batch
     (128, 2048, 128, "e4m3"),
