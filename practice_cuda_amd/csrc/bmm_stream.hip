@@ -165,14 +165,13 @@ __global__ __launch_bounds__(NT, 1) void bmm_stream_kernel(StreamArgs s) {
     // wave left before the barrier that ended the previous unit
     if (has_next) issue_unit(u + 1, st ^ 1);
 
-    v4f acc[4][8];
+    // the wave's eight B fragments (its 128 columns), held for the unit; each
+    // epilogue round below issues the MFMAs of its own 16 rows, so the
+    // matrix work is spread between the rounds' stores
+    v8i bf[8];
     const uint8_t* bt = smem + B_LDS + (wn >> 1) * (128 * 256);
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const v8i bf = lds::frag_mn<256>(bt, (wn & 1) * 128 + 16 * j, lane);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) acc[i][j] = mfma<FMT>(bf, af[i]);
-    }
+    for (int j = 0; j < 8; ++j) bf[j] = lds::frag_mn<256>(bt, (wn & 1) * 128 + 16 * j, lane);
 
     // crossing into the next batch: once every wave has read this batch's
     // B (its fragment reads complete), load the next one behind the stores
@@ -182,24 +181,28 @@ __global__ __launch_bounds__(NT, 1) void bmm_stream_kernel(StreamArgs s) {
       issue_b((u + 1) / s.units_per_batch);
     }
 
-    // epilogue: four rounds through the workgroup's 32 KiB of staging, which
-    // holds 32 whole rows of C (1 KiB each; 16-byte chunk c of staged row s
-    // at position c ^ (s & 15)). In round i, wave (wm, wn) stages rows
-    // 16 i .. 16 i + 15 of its 64 x 128 block as staged rows 16 wm + lr;
-    // after a barrier, wave w stores staged rows 4 w .. 4 w + 3, one whole
-    // 1 KiB row of C per instruction (non-temporal stores: plain ones, which
-    // keep C in L2, made config 4 12 us slower). Whole rows measured 3 us
-    // faster at config 4 than four 256-byte row pieces per instruction.
+    // Four rounds through the workgroup's 32 KiB of staging, which holds 32
+    // whole rows of C (1 KiB each; 16-byte chunk c of staged row s at
+    // position c ^ (s & 15)). In round i, wave (wm, wn) computes rows
+    // 16 i .. 16 i + 15 of its 64 x 128 block (8 MFMAs) and stages them as
+    // staged rows 16 wm + lr; after a barrier, wave w stores staged rows
+    // 4 w .. 4 w + 3, one whole 1 KiB row of C per instruction (non-temporal
+    // stores: plain ones, which keep C in L2, made config 4 12 us slower).
+    // Whole rows measured 3 us faster at config 4 than four 256-byte row
+    // pieces per instruction, and the MFMAs spread over the rounds 0.6 us
+    // faster than all 32 issued before the first.
     __bf16* cb = reinterpret_cast<__bf16*>(a.c) + int64_t(bidx) * a.scb;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
+      v4f acc[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc[j] = mfma<FMT>(bf[j], af[i]);
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         const float f = sav[i] * sbv[j];  // (sa * sb), then * P
         const int chunk = wn * 16 + 2 * j + (lg >> 1);
         uint2* dst = reinterpret_cast<uint2*>(stg + (wm * 16 + lr) * 1024 + ((chunk ^ lr) << 4) + ((lg & 1) << 3));
-        *dst = make_uint2(pack_bf16_pair(acc[i][j][0] * f, acc[i][j][1] * f),
-                          pack_bf16_pair(acc[i][j][2] * f, acc[i][j][3] * f));
+        *dst = make_uint2(pack_bf16_pair(acc[j][0] * f, acc[j][1] * f), pack_bf16_pair(acc[j][2] * f, acc[j][3] * f));
       }
       wait_lds();
       barrier();
@@ -212,8 +215,12 @@ __global__ __launch_bounds__(NT, 1) void bmm_stream_kernel(StreamArgs s) {
         const int mm = m0 + (srow >> 4) * 64 + 16 * i + (srow & 15);
         if (mm < a.m) __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(cb + int64_t(mm) * a.scm + 8 * chunk));
       }
-      wait_lds();
-      barrier();
+      // the next round overwrites the staging: every wave's reads first (the
+      // last round's reads are covered by the barrier that ends the unit)
+      if (i < 3) {
+        wait_lds();
+        barrier();
+      }
     }
 
     if (has_next) {
