@@ -16,9 +16,9 @@
 //     after the first unit no CU waits on a load with no stores in flight;
 //   - C leaves through LDS staging as whole 1 KiB rows, one row per store
 //     instruction.
-// Every load in the loop is an asynchronous global -> LDS copy issued from
-// inline asm, and the only compiler-visible memory operations are the C
-// stores, which nothing waits for. The loop's vmcnt waits are therefore
+// Every global memory access in the loop is inline asm (asynchronous
+// global -> LDS copies, and the C stores, which nothing waits for), so the
+// compiler tracks none of them and the loop's vmcnt waits are
 // written by hand: a unit's loads were issued before the previous unit's
 // 16 stores, so vmcnt(16) (vmcnt(0) after a partial unit) means they landed
 // without waiting for those stores.
@@ -77,6 +77,15 @@ PCAMD_DEV v4f mfma(const v8i& x, const v8i& y) {
 }
 
 PCAMD_DEV void barrier() { asm volatile("s_barrier" ::: "memory"); }
+
+// 16 bytes of C: a non-temporal vector store with device scope (nt sc1).
+// Measured at config 4 over five alternating runs: 48.1 us against 49.0 us
+// for the compiler's non-temporal store (nt alone); stores that allocate in
+// L2 (no nt, with or without a scope) took 64 us.
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+PCAMD_DEV void store_c(const u32x4& v, __bf16* p) {
+  asm volatile("global_store_dwordx4 %0, %1, off nt sc1" ::"v"(p), "v"(v) : "memory");
+}
 PCAMD_DEV void wait_lds() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
 
 struct StreamArgs {
@@ -186,11 +195,10 @@ __global__ __launch_bounds__(NT, 1) void bmm_stream_kernel(StreamArgs s) {
     // position c ^ (s & 15)). In round i, wave (wm, wn) computes rows
     // 16 i .. 16 i + 15 of its 64 x 128 block (8 MFMAs) and stages them as
     // staged rows 16 wm + lr; after a barrier, wave w stores staged rows
-    // 4 w .. 4 w + 3, one whole 1 KiB row of C per instruction (non-temporal
-    // stores: plain ones, which keep C in L2, made config 4 12 us slower).
-    // Whole rows measured 3 us faster at config 4 than four 256-byte row
-    // pieces per instruction, and the MFMAs spread over the rounds 0.6 us
-    // faster than all 32 issued before the first.
+    // 4 w .. 4 w + 3, one whole 1 KiB row of C per instruction. Whole rows
+    // measured 3 us faster at config 4 than four 256-byte row pieces per
+    // instruction, and the MFMAs spread over the rounds 0.6 us faster than
+    // all 32 issued before the first.
     __bf16* cb = reinterpret_cast<__bf16*>(a.c) + int64_t(bidx) * a.scb;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -208,12 +216,11 @@ __global__ __launch_bounds__(NT, 1) void bmm_stream_kernel(StreamArgs s) {
       barrier();
 #pragma unroll
       for (int it = 0; it < 4; ++it) {
-        typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
         const int srow = 4 * wave + it;
         const u32x4 v = *reinterpret_cast<const u32x4*>(stg + srow * 1024 + (lane << 4));
         const int chunk = lane ^ (srow & 15);
         const int mm = m0 + (srow >> 4) * 64 + 16 * i + (srow & 15);
-        if (mm < a.m) __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(cb + int64_t(mm) * a.scm + 8 * chunk));
+        if (mm < a.m) store_c(v, cb + int64_t(mm) * a.scm + 8 * chunk);
       }
       // the next round overwrites the staging: every wave's reads first (the
       // last round's reads are covered by the barrier that ends the unit)
