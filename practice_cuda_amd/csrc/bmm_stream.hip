@@ -233,6 +233,7 @@ __global__ __launch_bounds__(NT, 1) void bmm_stream_kernel(StreamArgs s) {
     if (has_next) {
       // this wave's loads for the next unit were issued before its 16 stores
       // (before fewer of them if rows past M were skipped: then wait for all)
+      static_assert(4 * 4 == kStoresPerUnit, "vmcnt(16) counts 4 rounds x 4 row stores per wave");
       if (m0 + UM <= a.m) asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
       else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
       wait_lds();
