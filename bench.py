@@ -82,6 +82,9 @@ def parse():
                    help="the config-5 GEMM shapes with tensor and row/column scales, this build's kernels "
                         "next to hipBLASLt (torch._scaled_mm): 'graph' times them (HIP graphs, one JSON "
                         "line), 'eager' launches each 3 times for rocprofv3 passes")
+    p.add_argument("--repack", action="store_true",
+                   help="the transpose variants' operand copy at the config-5 shapes: torch's strided "
+                        "copy (the reference's .contiguous()) next to pcamd_repack_fp8 (one JSON line)")
     return p.parse_args()
 
 
@@ -740,6 +743,33 @@ def mem_ceiling(torch, dev, steps, warmup):
     print(json.dumps({"mem_ceiling": res}))
 
 
+def repack_probe(torch, dev, steps, warmup):
+    """The copies behind the transpose BMM variants (an M-major A or an
+    N-major B made K-major) at the config-5 operand shapes, graph-timed over
+    rotating buffers: torch's copy of the strided fp8 view (what the
+    reference's `.contiguous()` runs) and pcamd_repack_fp8. Both must give
+    the same bytes; GB/s counts the bytes read and written."""
+    from practice_cuda_amd.impls._common import repack_rows_major
+    res = {}
+    for name, (rows, cols) in {"dgrad_B_W_14336x4096": (4096, 14336), "wgrad_A_dY_8192x14336": (14336, 8192),
+                               "X_8192x4096": (4096, 8192)}.items():
+        nsets = 3
+        g = torch.Generator(device=dev).manual_seed(rows + cols)
+        srcs = [torch.randint(0, 256, (cols, rows), generator=g, device=dev, dtype=torch.uint8)
+                .view(torch.float8_e4m3fn).t() for _ in range(nsets)]   # [rows, cols], stride(-2) == 1
+        dsts = [torch.empty(rows, cols, dtype=torch.float8_e4m3fn, device=dev) for _ in range(nsets)]
+        ms_t, _ = graph_time(torch, lambda i: dsts[i % nsets].copy_(srcs[i % nsets]), steps, warmup)
+        ms_h, _ = graph_time(torch, lambda i: repack_rows_major(srcs[i % nsets][None]), steps, warmup)
+        same = torch.equal(repack_rows_major(srcs[0][None])[0].view(torch.uint8), srcs[0].contiguous().view(torch.uint8))
+        nbytes = 2 * rows * cols
+        res[name] = {"torch_copy_ms": ms_t, "repack_ms": ms_h, "bytes": nbytes,
+                     "torch_copy_GB/s": nbytes / (ms_t * 1e-3) / 1e9, "repack_GB/s": nbytes / (ms_h * 1e-3) / 1e9,
+                     "identical": same}
+        del srcs, dsts
+        torch.cuda.empty_cache()
+    print(json.dumps({"repack": res}))
+
+
 def gemm_ref(torch, dev, steps, warmup, eager):
     """Reference point for the config-5 GEMMs: the same three products with
     per-tensor scales and the forward with row / column scales, run by this
@@ -837,6 +867,9 @@ def main():
         return
     if args.gemm_ref:
         gemm_ref(torch, dev, args.steps, args.warmup, args.gemm_ref == "eager")
+        return
+    if args.repack:
+        repack_probe(torch, dev, args.steps, args.warmup)
         return
 
     x2 = make_config2(torch)

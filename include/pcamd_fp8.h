@@ -19,6 +19,9 @@
  *                          and kernels/fp8_bmm/fp8_warper.py:9-77
  *   pcamd_bmm_quant_a   <- kernels/fp8_bmm/kernel/fp8_quant_bmm_fused_kernel.py:30-146
  *                          (its intent: the activation quantized inside the GEMM)
+ *   pcamd_repack_fp8    <- the `.contiguous()` copies of the do_transpose_a /
+ *                          do_transpose_b BMM variants
+ *                          (impls/triton_per_block.py:254-272)
  *   pcamd_bmm_scaled    <- impls/triton_per_block.py:232-420 (block scales),
  *                          impls/triton_per_channel.py:271-427 (channel scales),
  *                          impls/triton_per_tensor.py:140-306 and
@@ -183,6 +186,20 @@ int pcamd_bmm_quant_a(const void *a, int a_dtype, const void *b, int ab_dtype,
                       int64_t sqab, int64_t sqam, int64_t sqak, float *sa_out,
                       int64_t soab, int64_t soam, int64_t soak, float fp8_max,
                       float eps, int activation, void *stream);
+
+/*
+ * Transposing byte copy of an fp8 tensor: y[b, r, c] = x[b, r, c] for a
+ * view x contiguous along rows (sxr == 1) into a view y contiguous along
+ * columns (syc == 1); strides in elements (= bytes). This is the copy of the
+ * BMM wrappers' transpose variants - an M-major A made K-major, or an
+ * N-major B made K-major - that the reference makes with `.contiguous()`
+ * on the strided view (fp8_training/fp8_bench/impls/triton_per_block.py:
+ * 254-272). Other stride patterns return PCAMD_ERR_UNSUPPORTED.
+ */
+int pcamd_repack_fp8(const void *x, int64_t batch, int64_t rows,
+                     int64_t cols, int64_t sxb, int64_t sxr, int64_t sxc,
+                     void *y, int64_t syb, int64_t syr, int64_t syc,
+                     void *stream);
 
 #ifdef __cplusplus
 }

@@ -39,6 +39,7 @@ EXPORTED_SYMBOLS = (
     "pcamd_quant_tensor",
     "pcamd_bmm_scaled",
     "pcamd_bmm_quant_a",
+    "pcamd_repack_fp8",
 )
 # test-only entry points (include/pcamd_fp8_selftest.h), exported by the same library
 TEST_SYMBOLS = ("pcamd_selftest_fp8_convert",)
@@ -79,6 +80,8 @@ def _declare(lib: ctypes.CDLL) -> None:
         [_ptr, _int, _ptr, _int] + [_i64] * 4 + [_i64] * 6 + [_ptr, _int] + [_i64] * 3
         + [_ptr, _int] + [_i64] * 3 + [_ptr] + [_i64] * 3 + [_i64]
         + [_ptr] + [_i64] * 3 + [_ptr] + [_i64] * 3 + [_flt, _flt, _int, _ptr])
+    lib.pcamd_repack_fp8.restype = _int
+    lib.pcamd_repack_fp8.argtypes = [_ptr] + [_i64] * 6 + [_ptr] + [_i64] * 3 + [_ptr]
     lib.pcamd_selftest_fp8_convert.restype = _int
     lib.pcamd_selftest_fp8_convert.argtypes = [_int, _ptr, _ptr]
 

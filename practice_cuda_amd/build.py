@@ -18,7 +18,7 @@ CSRC = os.path.join(PKG_DIR, "csrc")
 BUILD_DIR = os.path.join(PKG_DIR, "_build")
 LIB_NAME = "libpcamd_fp8.so"
 LIB_PATH = os.path.join(BUILD_DIR, LIB_NAME)
-SOURCES = ["abi.hip", "quant.hip", "bmm.hip", "bmm_fast.hip", "bmm_wide.hip", "bmm_stream.hip"]
+SOURCES = ["abi.hip", "quant.hip", "bmm.hip", "bmm_fast.hip", "bmm_wide.hip", "bmm_stream.hip", "repack.hip"]
 
 ARCH = os.environ.get("PCAMD_OFFLOAD_ARCH", "gfx950")
 

@@ -59,6 +59,18 @@ struct Chunk {
 
 typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
 
+// 4 x 4 byte transpose: byte j of d[i] -> byte i of e[j]
+PCAMD_DEV void byte_transpose4(uint32_t d0, uint32_t d1, uint32_t d2, uint32_t d3, uint32_t (&e)[4]) {
+  const uint32_t lo01 = __builtin_amdgcn_perm(d1, d0, 0x05010400u);  // d0.b0 d1.b0 d0.b1 d1.b1
+  const uint32_t hi01 = __builtin_amdgcn_perm(d1, d0, 0x07030602u);  // d0.b2 d1.b2 d0.b3 d1.b3
+  const uint32_t lo23 = __builtin_amdgcn_perm(d3, d2, 0x05010400u);
+  const uint32_t hi23 = __builtin_amdgcn_perm(d3, d2, 0x07030602u);
+  e[0] = __builtin_amdgcn_perm(lo23, lo01, 0x05040100u);
+  e[1] = __builtin_amdgcn_perm(lo23, lo01, 0x07060302u);
+  e[2] = __builtin_amdgcn_perm(hi23, hi01, 0x05040100u);
+  e[3] = __builtin_amdgcn_perm(hi23, hi01, 0x07060302u);
+}
+
 // Input chunks are read once: non-temporal loads.
 template <int DT>
 PCAMD_DEV void load_chunk(Chunk<DT>& c, const void* p) {

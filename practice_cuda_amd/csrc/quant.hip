@@ -859,18 +859,6 @@ struct DualArgs {
   float fp8_max, eps;
 };
 
-// 4 x 4 byte transpose: byte j of d[i] -> byte i of e[j]
-PCAMD_DEV void byte_transpose4(uint32_t d0, uint32_t d1, uint32_t d2, uint32_t d3, uint32_t (&e)[4]) {
-  const uint32_t lo01 = __builtin_amdgcn_perm(d1, d0, 0x05010400u);  // d0.b0 d1.b0 d0.b1 d1.b1
-  const uint32_t hi01 = __builtin_amdgcn_perm(d1, d0, 0x07030602u);  // d0.b2 d1.b2 d0.b3 d1.b3
-  const uint32_t lo23 = __builtin_amdgcn_perm(d3, d2, 0x05010400u);
-  const uint32_t hi23 = __builtin_amdgcn_perm(d3, d2, 0x07030602u);
-  e[0] = __builtin_amdgcn_perm(lo23, lo01, 0x05040100u);
-  e[1] = __builtin_amdgcn_perm(lo23, lo01, 0x07060302u);
-  e[2] = __builtin_amdgcn_perm(hi23, hi01, 0x05040100u);
-  e[3] = __builtin_amdgcn_perm(hi23, hi01, 0x07060302u);
-}
-
 // Grid (128-column strips, 128-row groups, batch), NT threads. Lane t holds
 // columns 8 (t % 16) .. + 7 of rows t / 16 + (NT / 16) p (p < 2048 / NT) of
 // the 128 x 128 block, loaded up front (TCOL: rows 4 (t / 16) + p, p < 4).

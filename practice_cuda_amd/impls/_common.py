@@ -90,6 +90,25 @@ def dims3(x: torch.Tensor, y: torch.Tensor):
     return b, m, n, tuple(x.stride()), tuple(y.stride())
 
 
+def repack_rows_major(x: torch.Tensor) -> torch.Tensor:
+    """Contiguous copy of a 3-D fp8 view that is contiguous along dim -2: the
+    transposing copy of the do_transpose_a / do_transpose_b variants
+    (reference: `.contiguous()` of the strided view,
+    fp8_training/fp8_bench/impls/triton_per_block.py:254-272), made on the GPU
+    by pcamd_repack_fp8. Tensors off the GPU take torch's copy."""
+    if not x.is_cuda or x.stride(-2) != 1 or x.element_size() != 1 or min(x.shape[-2:]) <= 1:
+        return x.contiguous()  # also a single row / column: its other stride is arbitrary
+    y = torch.empty(x.shape, dtype=x.dtype, device=x.device)
+    if y.numel() == 0:
+        return y
+    bsz, rows, cols = x.shape
+    rc = _lib.lib().pcamd_repack_fp8(
+        _lib.ptr(x), bsz, rows, cols, x.stride(0) if bsz > 1 else 0, x.stride(1), x.stride(2),
+        _lib.ptr(y), y.stride(0), y.stride(1), y.stride(2), _lib.stream_of(y))
+    _lib.check(rc, "pcamd_repack_fp8")
+    return y
+
+
 def prepare_operands(a: QuantResult, b: QuantResult, do_transpose_a: bool, do_transpose_b: bool,
                      activation: str, b_layout_fn=matrix_layout):
     """Shared BMM front end (reference impls/triton_per_block.py:245-292)."""
@@ -103,7 +122,7 @@ def prepare_operands(a: QuantResult, b: QuantResult, do_transpose_a: bool, do_tr
         if in_a != "m-major":
             raise ValueError(
                 f"do_transpose_a=True requires an M-major A input; strides={a.tensor.stride()}")
-        a_tensor = a.tensor.contiguous()
+        a_tensor = repack_rows_major(a.tensor)
     else:
         a_tensor = a.tensor
 
@@ -115,7 +134,7 @@ def prepare_operands(a: QuantResult, b: QuantResult, do_transpose_a: bool, do_tr
         if in_b != "n-major":
             raise ValueError(
                 f"do_transpose_b=True requires an N-major B input; strides={b.tensor.stride()}")
-        b_tensor = b.tensor.transpose(-1, -2).contiguous().transpose(-1, -2)
+        b_tensor = repack_rows_major(b.tensor.transpose(-1, -2)).transpose(-1, -2)
     else:
         b_tensor = b.tensor
 

@@ -100,3 +100,26 @@ def test_bmm_invalid_arguments(over, msg):
 
 def test_bmm_empty_is_ok():
     assert _bmm(M=0) == 0
+
+
+def _repack(**over):
+    args = dict(x=FAKE, b=1, r=256, c=128, sxb=0, sxr=1, sxc=256, y=FAKE, syb=0, syr=128, syc=1, st=None)
+    args.update(over)
+    return _lib.lib().pcamd_repack_fp8(*args.values())
+
+
+@pytest.mark.parametrize("over,rc,msg", [
+    (dict(r=-1), -1, b"negative size"),
+    (dict(x=None), -1, b"null pointer"),
+    (dict(sxr=2), -2, b"contiguous along rows"),
+    (dict(syc=4), -2, b"contiguous along columns"),
+    (dict(sxc=100), -1, b"overlap"),
+    (dict(b=70000), -2, b"grid too large"),
+])
+def test_repack_invalid_arguments(over, rc, msg):
+    assert _repack(**over) == rc
+    assert msg in _lib.lib().pcamd_last_error()
+
+
+def test_repack_empty_is_ok():
+    assert _repack(r=0) == 0 and _repack(c=0) == 0 and _repack(b=0) == 0

@@ -1,0 +1,73 @@
+"""GPU parity of the fp8 repack (pcamd_repack_fp8, csrc/repack.hip).
+
+The BMM wrappers' transpose variants copy an M-major A or an N-major B into
+K-major order before the GEMM; the reference does it with `.contiguous()` on
+the strided view (fp8_training/fp8_bench/impls/triton_per_block.py:254-272).
+The repack moves the same bytes, so its output must equal torch's copy bit
+for bit: whole 128 x 128 tiles, ragged edges (rows and columns not multiples
+of 16 or 128), batches with padded batch strides, views that are not 16-byte
+aligned (the byte path), both fp8 formats, and the operand preparation of
+the transpose variants through the registry.
+"""
+from __future__ import annotations
+
+import pytest
+import torch
+
+from practice_cuda_amd.impls._common import repack_rows_major
+
+pytestmark = pytest.mark.gpu
+
+
+def _rows_major(dev, bsz, rows, cols, dtype, seed, pad_rows=0, pad_batch=0, offset=0):
+    """A [bsz, rows, cols] fp8 view contiguous along rows (stride(-2) == 1),
+    over storage with padded column pitch / batch pitch and a byte offset."""
+    g = torch.Generator(device=dev).manual_seed(seed)
+    pitch = rows + pad_rows
+    bpitch = cols * pitch + pad_batch
+    raw = torch.randint(0, 256, (offset + bsz * bpitch,), generator=g, device=dev, dtype=torch.uint8)
+    return raw.view(dtype).as_strided((bsz, rows, cols), (bpitch, 1, pitch), offset)
+
+
+CASES = [
+    # (bsz, rows, cols, pad_rows, pad_batch, offset)
+    (1, 8192, 4096, 0, 0, 0),        # config-5 X: whole tiles
+    (1, 4096, 14336, 0, 0, 0),
+    (3, 200, 333, 0, 0, 0),          # ragged both ways
+    (2, 77, 130, 3, 5, 0),           # not multiples of 16, padded pitches (byte path)
+    (2, 256, 256, 16, 32, 0),        # padded but 16-byte aligned pitches
+    (1, 512, 640, 0, 0, 1),          # unaligned base (byte path)
+    (1, 1000, 1, 0, 0, 0),           # one column
+]
+
+
+@pytest.mark.parametrize("fmt", [torch.float8_e4m3fn, torch.float8_e5m2])
+@pytest.mark.parametrize("bsz,rows,cols,pad_rows,pad_batch,offset", CASES)
+def test_repack_equals_torch_copy(dev, fmt, bsz, rows, cols, pad_rows, pad_batch, offset):
+    print(f"repack {bsz}x{rows}x{cols} pads {pad_rows},{pad_batch} offset {offset} {fmt}", flush=True)
+    x = _rows_major(dev, bsz, rows, cols, fmt, rows + cols, pad_rows, pad_batch, offset)
+    assert x.stride(-2) == 1
+    y = repack_rows_major(x)
+    ref = x.contiguous()
+    assert y.is_contiguous() and y.shape == x.shape and y.dtype == fmt
+    assert torch.equal(y.view(torch.uint8), ref.view(torch.uint8))
+
+
+def test_transpose_variants_use_repacked_operands(dev):
+    """The registry's transpose variants give the same result as the plain
+    layouts on the same values (their operands are repacked copies)."""
+    from practice_cuda_amd import get_bmm, get_quant
+    g = torch.Generator().manual_seed(9)
+    a = torch.randn(2, 384, 512, generator=g).bfloat16().to(dev)
+    b = torch.randn(2, 512, 640, generator=g).bfloat16().to(dev)
+    plain = get_bmm("hip_per_block_2d_a_k_b_n")
+    trans = get_bmm("hip_per_block_2d_a_k_b_n_transpose")
+    quant = get_quant(plain.quant_impl)
+    qa = quant.fn(a, block_m=1, block_n=128)
+    qb = quant.fn(b, **plain.quant_b_kwargs)
+    ref = plain.fn(qa, qb)
+    out = trans.fn(qa, qb)
+    # B N-major repacked to K-major: same math on the same values; the K-major
+    # and N-major kernels read the operands through different fragment paths
+    # but accumulate the same products in the same order
+    assert torch.equal(out.view(torch.int16), ref.view(torch.int16))
