@@ -71,3 +71,22 @@ def test_transpose_variants_use_repacked_operands(dev):
     # and N-major kernels read the operands through different fragment paths
     # but accumulate the same products in the same order
     assert torch.equal(out.view(torch.int16), ref.view(torch.int16))
+
+
+def test_repack_in_hip_graph(dev):
+    """Captured once, replayed three times with eager work between the
+    replays: every replay's output equals torch's copy of the current input."""
+    x = _rows_major(dev, 2, 640, 384, torch.float8_e4m3fn, 5, pad_rows=16)
+    s = torch.cuda.Stream(device=dev)
+    s.wait_stream(torch.cuda.current_stream(dev))
+    with torch.cuda.stream(s):
+        repack_rows_major(x)  # warm-up outside the capture
+    torch.cuda.current_stream(dev).wait_stream(s)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        y = repack_rows_major(x)
+    for it in range(3):
+        x.view(torch.uint8).copy_(torch.randint(0, 256, x.shape, device=dev, dtype=torch.uint8))  # new values
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(y.view(torch.uint8), x.contiguous().view(torch.uint8)), it
