@@ -653,8 +653,9 @@ def torch_eager_baseline(torch, sample, threads):
 
 
 def pmc_probe(torch, dev):
-    """Known-size copy (calibration) and the headline kernel, launched eagerly
-    so every dispatch carries its own counters."""
+    """Known-size copy (calibration), the headline kernel, then configs 1 and
+    3 (three dispatches each, rotating inputs), launched eagerly so every
+    dispatch carries its own counters."""
     from practice_cuda_amd import _lib as L
     src = torch.ones(1 << 27, dtype=torch.bfloat16, device=dev)  # 256 MiB
     dst = torch.empty_like(src)
@@ -670,8 +671,21 @@ def pmc_probe(torch, dev):
     for i in range(3):
         launch(i)
     torch.cuda.synchronize()
-    print(json.dumps({"copy_bytes_read": src.numel() * 2, "copy_bytes_written": dst.numel() * 2,
-                      "quant_bytes_read": x2.numel() * 2, "quant_bytes_written": x2.numel() + x2.shape[0] * 4}))
+    del xs, ys, ss
+    out = {"copy_bytes_read": src.numel() * 2, "copy_bytes_written": dst.numel() * 2,
+           "quant_bytes_read": x2.numel() * 2, "quant_bytes_written": x2.numel() + x2.shape[0] * 4}
+    for name, make, bm, bn in (("config1", make_config1, 1, 128), ("config3", make_config3, 128, 128)):
+        x = make(torch)
+        xs = rotate_sets(torch, x, 3, dev)
+        ys = [torch.empty(x.shape, dtype=torch.float8_e4m3fn, device=dev) for _ in range(3)]
+        ss = [torch.empty(-(-x.shape[0] // bm), -(-x.shape[1] // bn), device=dev) for _ in range(3)]
+        launch = quant_block_launcher(torch, L, xs, ys, ss, bm, bn)
+        for i in range(3):
+            launch(i)
+        torch.cuda.synchronize()
+        out[name] = {"bytes_read": x.numel() * 2, "bytes_written": x.numel() + ss[0].numel() * 4}
+        del xs, ys, ss
+    print(json.dumps(out))
 
 
 def pmc_probe_bmm(torch, dev):
