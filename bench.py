@@ -313,15 +313,27 @@ def bench_config4(torch, steps, warmup, dev, nsets=4):
                          "traffic": pmc_field("config4", CONFIG4_KERNEL, ("fetch_bytes", "write_bytes"))}}
 
 
+CONFIG5_DIMS = (8192, 4096, 14336)  # M (tokens), K (in features), N (out features)
+
+
+def config5_inputs(torch):
+    """BASELINE config 5 inputs on the host, CPU generator seed 0, in this
+    order: X [M, K] ~ N(0, 1), W [N, K] ~ N(0, 0.02), dY [M, N] ~ N(0, 1e-3),
+    all bf16. The GPU parity tests draw the same tensors."""
+    M, K, N = CONFIG5_DIMS
+    g = torch.Generator().manual_seed(0)
+    X = torch.randn(M, K, generator=g).bfloat16()
+    W = (torch.randn(N, K, generator=g) * 0.02).bfloat16()
+    dY = (torch.randn(M, N, generator=g) * 1e-3).bfloat16()
+    return X, W, dY
+
+
 def config5_operands(torch, dev):
     """BASELINE config 5 (M=8192 K=4096 N=14336), CPU generator seed 0:
     the bf16 tensors and their block quantizations."""
     from practice_cuda_amd.impls.hip_per_block import hip_per_block_quant
-    M, K, N = 8192, 4096, 14336
-    g = torch.Generator().manual_seed(0)
-    X = torch.randn(M, K, generator=g).bfloat16().to(dev)
-    W = (torch.randn(N, K, generator=g) * 0.02).bfloat16().to(dev)
-    dY = (torch.randn(M, N, generator=g) * 1e-3).bfloat16().to(dev)
+    M, K, N = CONFIG5_DIMS
+    X, W, dY = (t.to(dev) for t in config5_inputs(torch))
     q = {
         "x": hip_per_block_quant(X[None], block_m=1, block_n=128),      # [1, M, K] 1x128
         "w": hip_per_block_quant(W[None], block_m=128, block_n=128),    # [1, N, K] 128x128
@@ -906,6 +918,10 @@ def main():
         "config": {"workload": "BASELINE configs[1]: per-channel fp8 quant, bf16 weight [18432,7168] "
                                "-> e4m3 + fp32 row scales [18432], channel_axis=-2",
                    "shape": [18432, 7168], "rotating_buffer_sets": 4,
+                   "metric_halves": "value and roofline are the quantizer half of the metric (GB/s, % of HBM "
+                                    "peak); the FP8 BMM half is in components: config 5 (the block-scaled "
+                                    "GEMM trio) carries its own roofline block (TFLOP/s, % of dense fp8 "
+                                    "peak), config 4 one against HBM",
                    "timing": "HIP graph of K launches, median of 5 replays, after ~100 ms untimed settle "
                              "and W warmup launches"},
         "roofline": {"bound": "hbm", "achieved": round(head["value"], 2), "peak": HBM_PEAK_GBS,

@@ -21,6 +21,8 @@ _LIB = None
 F32, BF16, F16, E4M3FN, E5M2 = 0, 1, 2, 3, 4
 SCALE_BLOCK, SCALE_CHANNEL, SCALE_TENSOR = 0, 1, 2
 ACT_NONE, ACT_GELU = 0, 1
+# status codes (include/pcamd_fp8.h)
+OK, ERR_INVALID, ERR_UNSUPPORTED, ERR_LAUNCH = 0, -1, -2, -3
 
 _DTYPE_CODES = {
     torch.float32: F32,

@@ -54,7 +54,11 @@ constexpr int SA_LDS = A_LDS + 2 * UM * BK;  // two stages of 1 KiB (128 row sca
 constexpr int SB_LDS = SA_LDS + 2 * 1024;    // 1 KiB: the batch's column-block scales
 constexpr int STG_LDS = SB_LDS + 1024;       // output staging: 32 rows of C (1 KiB each)
 constexpr int LDS_BYTES = STG_LDS + WAVES * 4096;
-constexpr int kStoresPerUnit = 16;        // global store instructions per wave per unit
+constexpr int kRounds = 4;                // staging rounds per unit: one per 16-row block of a wave's 64 rows
+constexpr int kRowStoresPerRound = 4;     // whole 1 KiB rows of C stored per wave per round
+constexpr int kStoresPerUnit = kRounds * kRowStoresPerRound;  // global store instructions per wave per unit
+static_assert(kRounds * 16 == 64, "a round covers one 16-row block of the wave's 64 x 128 output block");
+static_assert(WAVES * kRowStoresPerRound == 32, "the staging holds 32 rows of C: every wave stores its share");
 
 // K-major A tile: chunk c (16 B) of row r at position c ^ swz(r)
 PCAMD_DEV int swz(int r) { return (r ^ (r >> 4)) & 7; }
@@ -201,7 +205,7 @@ __global__ __launch_bounds__(NT, 1) void bmm_stream_kernel(StreamArgs s) {
     // all 32 issued before the first.
     __bf16* cb = reinterpret_cast<__bf16*>(a.c) + int64_t(bidx) * a.scb;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < kRounds; ++i) {
       v4f acc[8];
 #pragma unroll
       for (int j = 0; j < 8; ++j) acc[j] = mfma<FMT>(bf[j], af[i]);
@@ -215,8 +219,8 @@ __global__ __launch_bounds__(NT, 1) void bmm_stream_kernel(StreamArgs s) {
       wait_lds();
       barrier();
 #pragma unroll
-      for (int it = 0; it < 4; ++it) {
-        const int srow = 4 * wave + it;
+      for (int it = 0; it < kRowStoresPerRound; ++it) {
+        const int srow = kRowStoresPerRound * wave + it;
         const u32x4 v = *reinterpret_cast<const u32x4*>(stg + srow * 1024 + (lane << 4));
         const int chunk = lane ^ (srow & 15);
         const int mm = m0 + (srow >> 4) * 64 + 16 * i + (srow & 15);
@@ -224,17 +228,17 @@ __global__ __launch_bounds__(NT, 1) void bmm_stream_kernel(StreamArgs s) {
       }
       // the next round overwrites the staging: every wave's reads first (the
       // last round's reads are covered by the barrier that ends the unit)
-      if (i < 3) {
+      if (i < kRounds - 1) {
         wait_lds();
         barrier();
       }
     }
 
     if (has_next) {
-      // this wave's loads for the next unit were issued before its 16 stores
-      // (before fewer of them if rows past M were skipped: then wait for all)
-      static_assert(4 * 4 == kStoresPerUnit, "vmcnt(16) counts 4 rounds x 4 row stores per wave");
-      if (m0 + UM <= a.m) asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
+      // this wave's loads for the next unit were issued before its
+      // kStoresPerUnit stores (before fewer of them if rows past M were
+      // skipped: then wait for all); the immediate is that same constant
+      if (m0 + UM <= a.m) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kStoresPerUnit) : "memory");
       else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
       wait_lds();
       barrier();

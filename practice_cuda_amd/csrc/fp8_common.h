@@ -247,12 +247,7 @@ PCAMD_DEV uint32_t hw_pack4(float a, float b, float c, float d) {
 
 template <int FMT>
 PCAMD_DEV uint32_t pack4(float a, float b, float c, float d) {
-#ifdef PCAMD_SOFTWARE_FP8_CONVERT
-  return sw_encode<FMT>(a) | (sw_encode<FMT>(b) << 8) | (sw_encode<FMT>(c) << 16) |
-         (sw_encode<FMT>(d) << 24);
-#else
   return hw_pack4<FMT>(a, b, c, d);
-#endif
 }
 
 // tl.clamp(v, -max, max)
@@ -280,9 +275,11 @@ constexpr float fmt_max() {
 // fp8_max is the format's largest finite value and qs = fp8_max / s with s at
 // least the max |x| of the values it scales: then |fl(x * qs)| <= fp8_max *
 // (1 + 2^-23), below the rounding midpoint to the next (non-finite) code
-// (464 for e4m3fn, 59392 for e5m2), and round-to-nearest-even gives the
+// (464 for e4m3fn, 61440 for e5m2), and round-to-nearest-even gives the
 // clamped value's code. The conversion self-test pins the hardware converter
-// up to those midpoints.
+// on every pattern up to 464 (e4m3fn) and 59392 (e5m2), both past
+// fp8_max * (1 + 2^-23). The host picks these instantiations only when qs is
+// finite as well (clamp_free in quant.hip).
 template <int FMT, bool CLAMP>
 PCAMD_DEV uint2 quant8(const float (&v)[8], float qs, float fp8_max) {
   float q[8];
@@ -294,11 +291,7 @@ PCAMD_DEV uint2 quant8(const float (&v)[8], float qs, float fp8_max) {
 template <int DT, int FMT>
 PCAMD_DEV uint32_t quant_one(float v, float qs, float fp8_max) {
   float q = clamp_sym(v * qs, fp8_max);
-#ifdef PCAMD_SOFTWARE_FP8_CONVERT
-  return sw_encode<FMT>(q);
-#else
   return hw_pack4<FMT>(q, 0.0f, 0.0f, 0.0f) & 0xFFu;
-#endif
 }
 
 // Scale formulas of the reference kernels (IEEE fp32 division).

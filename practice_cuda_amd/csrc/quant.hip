@@ -44,6 +44,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <cmath>
 #include <cstdint>
 #include <cstdlib>
 
@@ -613,8 +614,9 @@ __global__ void tensor_finalize_kernel(TensorArgs a) {
 // ===========================================================================
 template <int FMT>
 __global__ __launch_bounds__(kThreads) void selftest_convert_kernel(uint32_t* result, uint32_t limit) {
-  // Every pattern p in [0, limit] (limit: bits of the rounding midpoint above
-  // the fp8 max) is converted
+  // Every pattern p in [0, limit] (limit: bits of 464.0 for e4m3fn, the
+  // rounding midpoint above its max, and of 59392.0 for e5m2, below the
+  // midpoint 61440) is converted
   // in lane position 0 of a packed quadruple (x, y, -x, w) with y and w drawn
   // from other patterns of the range, so sign handling and the byte order of
   // the packed result are checked along with the rounding.
@@ -1074,12 +1076,23 @@ inline bool nt_stores() {
   return v != 0;
 }
 
+// The clamp of the reference (tl.clamp before the cast) is left out of the
+// quantizers (quant8 in fp8_common.h) only when it cannot change a byte: at
+// the format's largest value, and with every quant scale qs = fp8_max /
+// max(amax, eps) finite, which holds for all amax when fp8_max / eps does.
+// Below that eps (fp8_max / FLT_MAX, about 1.3e-36 for e4m3fn) a group whose
+// amax is under the bound gets qs = inf, x * qs = +-inf, and only the clamp
+// turns that into +-fp8_max; eps <= 0 or NaN keeps the clamp too.
+template <int FMT>
+inline bool clamp_free(float fp8_max, float eps) {
+  return fp8_max == fmt_max<FMT>() && eps > 0.0f && std::isfinite(fp8_max / eps);
+}
+
 template <int DT, int FMT>
 struct LaunchGroups {
   template <int LPG, int CPL, bool NTS>
   static int go(const RowArgs& a, hipStream_t st) {
-    // the clamp is a no-op (and is left out) at the format's largest value
-    return a.fp8_max == fmt_max<FMT>() ? go2<LPG, CPL, NTS, false>(a, st) : go2<LPG, CPL, NTS, true>(a, st);
+    return clamp_free<FMT>(a.fp8_max, a.eps) ? go2<LPG, CPL, NTS, false>(a, st) : go2<LPG, CPL, NTS, true>(a, st);
   }
   template <int LPG, int CPL, bool NTS, bool CLAMP>
   static int go2(const RowArgs& a, hipStream_t st) {
@@ -1117,7 +1130,8 @@ template <int DT, int FMT>
 struct LaunchRowBlock {
   template <int CPT, bool NTS>
   static int go(const RowArgs& a, int threads, hipStream_t st) {
-    return a.fp8_max == fmt_max<FMT>() ? go2<CPT, NTS, false>(a, threads, st) : go2<CPT, NTS, true>(a, threads, st);
+    return clamp_free<FMT>(a.fp8_max, a.eps) ? go2<CPT, NTS, false>(a, threads, st)
+                                             : go2<CPT, NTS, true>(a, threads, st);
   }
   template <int CPT, bool NTS, bool CLAMP>
   static int go2(const RowArgs& a, int threads, hipStream_t st) {
@@ -1154,7 +1168,7 @@ template <int DT, int FMT>
 struct LaunchTile {
   template <int CPT, bool NTS>
   static int go(const TileArgs& a, hipStream_t st) {
-    return a.fp8_max == fmt_max<FMT>() ? go2<CPT, NTS, false>(a, st) : go2<CPT, NTS, true>(a, st);
+    return clamp_free<FMT>(a.fp8_max, a.eps) ? go2<CPT, NTS, false>(a, st) : go2<CPT, NTS, true>(a, st);
   }
   template <int CPT, bool NTS, bool CLAMP>
   static int go2(const TileArgs& a, hipStream_t st) {
@@ -1216,8 +1230,7 @@ struct LaunchDual {
                     static_cast<uint32_t>(batch));
     constexpr int NT = 512;  // 256: 3 % slower at [8192, 14336]; 1024: 4 % slower
     const bool full = a.m % 128 == 0 && a.n % 128 == 0;
-    // the clamp is a no-op (and is left out) at the format's largest value
-    if (a.fp8_max == fmt_max<FMT>()) return go2<NTS, false>(a, grid, full, tcol, st);
+    if (clamp_free<FMT>(a.fp8_max, a.eps)) return go2<NTS, false>(a, grid, full, tcol, st);
     return go2<NTS, true>(a, grid, full, tcol, st);
   }
   template <bool NTS, bool CLAMP>
@@ -1546,9 +1559,10 @@ extern "C" int pcamd_selftest_fp8_convert(int fmt, uint32_t* result, void* strea
   if (fmt != kE4M3 && fmt != kE5M2) return set_error(PCAMD_ERR_INVALID, "unknown fp8 format %d", fmt);
   hipStream_t st = static_cast<hipStream_t>(stream);
   selftest_init_kernel<<<1, 1, 0, st>>>(result);
-  // every pattern up to the rounding midpoint above the fp8 max (464 for
-  // e4m3fn, 59392 for e5m2), which both round to the max: the quantizers
-  // leave out the clamp when x * qs cannot exceed max * (1 + 2^-23)
+  // every pattern up to 464 for e4m3fn (the rounding midpoint above 448) and
+  // up to 59392 for e5m2 (below its midpoint 61440); both bounds round to
+  // the max and lie past max * (1 + 2^-23), the most x * qs can reach where
+  // the quantizers leave out the clamp
   if (fmt == kE4M3) selftest_convert_kernel<kE4M3><<<4096, kThreads, 0, st>>>(result, 0x43E80000u);
   else selftest_convert_kernel<kE5M2><<<4096, kThreads, 0, st>>>(result, 0x47680000u);
   return check_launch("selftest_convert_kernel");

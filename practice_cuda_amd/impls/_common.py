@@ -95,16 +95,25 @@ def repack_rows_major(x: torch.Tensor) -> torch.Tensor:
     transposing copy of the do_transpose_a / do_transpose_b variants
     (reference: `.contiguous()` of the strided view,
     fp8_training/fp8_bench/impls/triton_per_block.py:254-272), made on the GPU
-    by pcamd_repack_fp8. Tensors off the GPU take torch's copy."""
+    by pcamd_repack_fp8. Tensors off the GPU take torch's copy, and so do the
+    views the kernel does not take: a single row or column (its other stride
+    is arbitrary), columns that overlap the rows they step over (expanded
+    views), and shapes past the kernel's grid (PCAMD_ERR_UNSUPPORTED: more
+    than 65535 batches or 65535 x 128 rows)."""
     if not x.is_cuda or x.stride(-2) != 1 or x.element_size() != 1 or min(x.shape[-2:]) <= 1:
-        return x.contiguous()  # also a single row / column: its other stride is arbitrary
+        return x.contiguous()
     y = torch.empty(x.shape, dtype=x.dtype, device=x.device)
     if y.numel() == 0:
         return y
     bsz, rows, cols = x.shape
+    sxb = x.stride(0) if bsz > 1 else 0
+    if x.stride(2) < rows or sxb < 0:
+        return x.contiguous()
     rc = _lib.lib().pcamd_repack_fp8(
-        _lib.ptr(x), bsz, rows, cols, x.stride(0) if bsz > 1 else 0, x.stride(1), x.stride(2),
+        _lib.ptr(x), bsz, rows, cols, sxb, x.stride(1), x.stride(2),
         _lib.ptr(y), y.stride(0), y.stride(1), y.stride(2), _lib.stream_of(y))
+    if rc == _lib.ERR_UNSUPPORTED:
+        return x.contiguous()
     _lib.check(rc, "pcamd_repack_fp8")
     return y
 

@@ -203,7 +203,6 @@ def hip_per_block_bmm(
         _lib.SCALE_BLOCK, False, qbm, qbk, qbn, activation, batch, m, n, k)
 
 
-_UNSUPPORTED = -2  # PCAMD_ERR_UNSUPPORTED
 
 
 def hip_per_block_bmm_quant_a(
@@ -261,7 +260,7 @@ def hip_per_block_bmm_quant_a(
         qa = torch.empty((batch, m, k), device=x3.device, dtype=fp8_dtype)
         sa = torch.empty((batch, m, -(-k // 128)), device=x3.device, dtype=torch.float32)
     L = _lib.lib()
-    rc = _UNSUPPORTED
+    rc = _lib.ERR_UNSUPPORTED
     if in_b in ("n-major", "k-major") and x3.stride(-1) == 1:
         with torch.cuda.device(x3.device):
             rc = L.pcamd_bmm_quant_a(
@@ -274,7 +273,7 @@ def hip_per_block_bmm_quant_a(
                 _lib.ptr(sa), *(sa.stride() if sa is not None else (0, 0, 0)),
                 float(torch.finfo(fp8_dtype).max), float(eps),
                 _lib.ACT_GELU if activation == "gelu" else _lib.ACT_NONE, _lib.stream_of(x3))
-    if rc == _UNSUPPORTED:
+    if rc == _lib.ERR_UNSUPPORTED:
         qres = hip_per_block_quant(x3, block_m=1, block_n=128, fp8_dtype=fp8_dtype, eps=eps)
         hip_per_block_bmm(qres, b, out_dtype=out_dtype, bias=bias, out=out, activation=activation)
         if return_quant:

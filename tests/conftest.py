@@ -27,6 +27,18 @@ def pytest_collection_modifyitems(config, items):
 
 
 @pytest.fixture(scope="session")
+def config5_host():
+    """BASELINE config 5 inputs (X [8192, 4096], W [14336, 4096], dY [8192,
+    14336], bf16) from the CPU generator with seed 0: the tensors bench.py
+    times."""
+    import torch
+
+    import bench
+
+    return bench.config5_inputs(torch)
+
+
+@pytest.fixture(scope="session")
 def dev():
     import torch
 

@@ -276,6 +276,67 @@ def test_dual_matches_oracle(dev, shape, dtype, block, fmt, kind, col_t):
         assert r.dequant_scale.shape == one.dequant_scale.shape
 
 
+
+def _tiny_input(dtype, seed):
+    """[256, 512] of N(0, 1) in which one 128 x 128 block, row 200 and column
+    300 hold only values of magnitude 1.2e-38 .. 2e-38 (normal in fp32 and
+    bf16, random signs, no zeros): every kind of group, block, row and column
+    has a member whose amax is that small."""
+    g = np.random.default_rng(seed)
+    x = g.standard_normal((256, 512)).astype(np.float32)
+    def tiny(shape):
+        return (g.uniform(1.2e-38, 2e-38, shape) * g.choice([-1.0, 1.0], shape)).astype(np.float32)
+    x[:128, :128] = tiny((128, 128))
+    x[200, :] = tiny((512,))
+    x[:, 300] = tiny((256,))
+    return torch.from_numpy(x).to(DT[dtype])
+
+
+TINY_EPS_PATHS = [
+    # (kind, dtype, bm, bn)
+    ("block", "bf16", 1, 128),      # row groups, flat
+    ("block", "f32", 1, 128),
+    ("block", "bf16", 128, 128),    # tiles
+    ("block", "bf16", 128, 1),      # column groups
+    ("block", "bf16", 4, 16),       # generic
+    ("channel-2", "bf16", 0, 0),    # one scale per row
+    ("channel-1", "bf16", 0, 0),    # one scale per column
+    ("dual", "bf16", 0, 0),
+    ("dual_t", "bf16", 0, 0),
+]
+
+
+@pytest.mark.parametrize("fmt", ["e4m3", "e5m2"])
+@pytest.mark.parametrize("kind,dtype,bm,bn", TINY_EPS_PATHS)
+def test_eps_zero_tiny_amax_matches_oracle(dev, kind, dtype, bm, bn, fmt):
+    """eps = 0 with groups whose amax is below fp8_max / FLT_MAX: qs = fp8_max /
+    amax overflows to inf, x * qs = +-inf, and the reference's clamp makes
+    that +-fp8_max. The clamp-free kernel instantiations would emit NaN (e4m3)
+    or inf (e5m2) bytes there, so the host keeps the clamp; bit-exact against
+    the oracle at the format maximum."""
+    fmax = 448.0 if fmt == "e4m3" else 57344.0
+    print(f"eps=0 tiny amax {kind} {dtype} {bm}x{bn} {fmt}", flush=True)
+    x = _tiny_input(dtype, seed=bm + bn + len(kind))
+    xd = x.to(dev)
+    fp8 = FMT[fmt]
+    if kind == "block":
+        q, s = _abi_quant_block(xd, bm, bn, fp8, fmax, eps=0.0)
+        _same_bits(q, s, *O.quant_block(x, bm, bn, fmt=fmt, eps=0.0), kind)
+    elif kind.startswith("channel"):
+        axis = int(kind[len("channel"):])
+        q, s = _abi_quant_channel(xd, axis, fp8, fmax, eps=0.0)
+        _same_bits(q, s, *O.quant_channel(x, axis, fmt=fmt, eps=0.0), kind)
+    else:
+        yr, sr, yc, sc = _abi_quant_dual(xd, fp8, fmax, kind == "dual_t", eps=0.0)
+        q1, s1 = O.quant_block(x, 1, 128, fmt=fmt, eps=0.0)
+        q2, s2 = O.quant_block(x, 128, 1, fmt=fmt, eps=0.0)
+        _same_bits(yr, sr, q1, s1, kind + " rows")
+        _same_bits(yc, sc, q2, s2, kind + " columns")
+    # the tiny elements saturate: no NaN / inf code anywhere
+    qb = qbits(q if kind == "block" or kind.startswith("channel") else yr)
+    nan_codes = (0x7F, 0xFF) if fmt == "e4m3" else tuple(range(0x7C, 0x80)) + tuple(range(0xFC, 0x100))
+    assert not np.isin(qb, nan_codes).any()
+
 def test_dual_full_size(dev):
     """Both quantizations of the config-1 input shape (bf16 [4096, 7168],
     N(0,1) with 0.1% outliers x50) from one kernel, bit-exact."""
@@ -447,18 +508,18 @@ def _planted_input(shape, dtype, fmax, seed):
     return torch.from_numpy(x).to(DT[dtype])
 
 
-def _abi_quant_block(xd, bm, bn, fp8, fmax):
+def _abi_quant_block(xd, bm, bn, fp8, fmax, eps=1e-12):
     y = torch.empty_like(xd, dtype=fp8)
     x3, y3 = (xd[None], y[None]) if xd.ndim == 2 else (xd, y)
     b, m, n = x3.shape
     s = torch.empty(b, -(-m // bm), -(-n // bn), device=xd.device)
     _lib.check(_lib.lib().pcamd_quant_block(
         _lib.ptr(x3), _lib.dtype_code(xd.dtype), b, m, n, *x3.stride(), _lib.ptr(y3), _lib.dtype_code(fp8),
-        *y3.stride(), _lib.ptr(s), *s.stride(), bm, bn, float(fmax), 1e-12, _lib.stream_of(xd)), "quant_block")
+        *y3.stride(), _lib.ptr(s), *s.stride(), bm, bn, float(fmax), float(eps), _lib.stream_of(xd)), "quant_block")
     return y, s
 
 
-def _abi_quant_dual(xd, fp8, fmax, transposed):
+def _abi_quant_dual(xd, fp8, fmax, transposed, eps=1e-12):
     x3 = xd[None] if xd.ndim == 2 else xd
     b, m, n = x3.shape
     yr = torch.empty_like(x3, dtype=fp8)
@@ -472,18 +533,18 @@ def _abi_quant_dual(xd, fp8, fmax, transposed):
     _lib.check(_lib.lib().pcamd_quant_block_dual(
         _lib.ptr(x3), _lib.dtype_code(xd.dtype), b, m, n, *x3.stride(), _lib.ptr(yr), *yr.stride(),
         _lib.ptr(yc), *yc.stride(), _lib.dtype_code(fp8), _lib.ptr(sr), *sr.stride(), _lib.ptr(sc),
-        *sc.stride(), 128, float(fmax), 1e-12, _lib.stream_of(xd)), "quant_block_dual")
+        *sc.stride(), 128, float(fmax), float(eps), _lib.stream_of(xd)), "quant_block_dual")
     return yr, sr, yc, sc
 
 
-def _abi_quant_channel(xd, axis, fp8, fmax):
+def _abi_quant_channel(xd, axis, fp8, fmax, eps=1e-12):
     y = torch.empty_like(xd, dtype=fp8)
     x3, y3 = (xd[None], y[None]) if xd.ndim == 2 else (xd, y)
     b, m, n = x3.shape
     s = torch.empty(b, m if axis == -2 else n, device=xd.device)
     _lib.check(_lib.lib().pcamd_quant_channel(
         _lib.ptr(x3), _lib.dtype_code(xd.dtype), b, m, n, *x3.stride(), _lib.ptr(y3), _lib.dtype_code(fp8),
-        *y3.stride(), _lib.ptr(s), *s.stride(), axis, float(fmax), 1e-12, _lib.stream_of(xd)), "quant_channel")
+        *y3.stride(), _lib.ptr(s), *s.stride(), axis, float(fmax), float(eps), _lib.stream_of(xd)), "quant_channel")
     return y, s
 
 

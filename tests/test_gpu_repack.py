@@ -37,7 +37,10 @@ CASES = [
     (2, 77, 130, 3, 5, 0),           # not multiples of 16, padded pitches (byte path)
     (2, 256, 256, 16, 32, 0),        # padded but 16-byte aligned pitches
     (1, 512, 640, 0, 0, 1),          # unaligned base (byte path)
-    (1, 1000, 1, 0, 0, 0),           # one column
+    (1, 1000, 2, 0, 0, 0),           # narrow: fewer columns than one 16-byte store,
+    (2, 333, 7, 0, 0, 0),            #   rows not multiples of 16 (per-byte masked stores)
+    (1, 77, 15, 5, 0, 0),
+    (3, 130, 9, 16, 8, 0),
 ]
 
 
@@ -90,3 +93,30 @@ def test_repack_in_hip_graph(dev):
         g.replay()
         torch.cuda.synchronize()
         assert torch.equal(y.view(torch.uint8), x.contiguous().view(torch.uint8)), it
+
+
+@pytest.mark.parametrize("case", ["one_column", "expanded_columns", "batch_past_grid"])
+def test_repack_fallback_to_torch_copy(dev, case):
+    """Views the kernel does not take go to torch's copy and still come back
+    contiguous and equal to it: a single column (its column stride is
+    arbitrary), columns that overlap the rows (an expanded view, column
+    stride 0) and more batches than the kernel's grid covers (the C entry
+    point returns PCAMD_ERR_UNSUPPORTED without launching)."""
+    from practice_cuda_amd import _lib
+    fmt = torch.float8_e4m3fn
+    print(f"repack fallback {case}", flush=True)
+    if case == "one_column":
+        x = _rows_major(dev, 1, 1000, 1, fmt, 3)
+    elif case == "expanded_columns":
+        x = _rows_major(dev, 2, 300, 1, fmt, 4).expand(2, 300, 40)
+        assert x.stride(-1) == 0
+    else:
+        x = _rows_major(dev, 70000, 2, 16, fmt, 5)
+        y = torch.empty(x.shape, dtype=fmt, device=dev)
+        rc = _lib.lib().pcamd_repack_fp8(_lib.ptr(x), 70000, 2, 16, x.stride(0), 1, x.stride(2), _lib.ptr(y),
+                                         *y.stride(), _lib.stream_of(y))
+        assert rc == _lib.ERR_UNSUPPORTED
+    assert x.stride(-2) == 1
+    y = repack_rows_major(x)
+    assert y.is_contiguous() and y.shape == x.shape
+    assert torch.equal(y.view(torch.uint8), x.contiguous().view(torch.uint8))

@@ -290,3 +290,25 @@ def test_bmm_golden():
     bias = torch.from_numpy(d["bias"].view(np.int16)).view(torch.bfloat16).float().numpy()
     ref = O.bmm_reference(O.dequant_block(qa, sa, 1, 128), O.dequant_block(qb, sb, 128, 128), bias)
     assert O.max_abs_rel(ref, d["expected"]) < 1e-6
+
+
+def test_eps_zero_tiny_amax_saturates():
+    """eps = 0 and a group whose amax is below fp8_max / FLT_MAX: the quant
+    scale fp8_max / amax overflows to inf, every x * qs is +-inf and the clamp
+    of the reference (kernels/quant/per_block.py:46-48) maps it to +-fp8_max;
+    the block dequant scale 1 / qs is 0 and the channel one amax / fp8_max
+    (per_channel.py:159-161) a subnormal."""
+    x = np.full((2, 128), 1.5e-38, np.float32)
+    x[:, 1::2] *= -1.0
+    assert not np.isfinite(f32(448.0) / f32(1.5e-38))
+    for fmt, pos, neg in (("e4m3", 0x7E, 0xFE), ("e5m2", 0x7B, 0xFB)):
+        q, s = O.quant_block(x, 1, 128, fmt=fmt, eps=0.0)
+        assert np.all(q[:, 0::2] == pos) and np.all(q[:, 1::2] == neg), fmt
+        assert np.all(s == 0.0)
+        q, s = O.quant_channel(x, -2, fmt=fmt, eps=0.0)
+        assert np.all(q[:, 0::2] == pos) and np.all(q[:, 1::2] == neg), fmt
+        fmax = 448.0 if fmt == "e4m3" else 57344.0
+        assert np.all(s == f32(1.5e-38) / f32(fmax)) and 0.0 < s[0] < np.finfo(np.float32).tiny
+    # a group of ordinary values beside it keeps finite, exact scales
+    q, s = O.quant_block(np.array([[1.0] * 128], np.float32), 1, 128, eps=0.0)
+    assert s[0, 0] == f32(1.0) / (f32(448.0) / f32(1.0)) and q[0, 0] == 0x7E
