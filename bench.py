@@ -82,6 +82,10 @@ def parse():
                    help="the config-5 GEMM shapes with tensor and row/column scales, this build's kernels "
                         "next to hipBLASLt (torch._scaled_mm): 'graph' times them (HIP graphs, one JSON "
                         "line), 'eager' launches each 3 times for rocprofv3 passes")
+    p.add_argument("--published", choices=["graph", "eager"], default=None,
+                   help="the reference's 31 published per-tensor fp8 BMM shapes (fp16 C + fp16 bias, "
+                        "B N-major / K-major as published): 'graph' times them (one JSON line), 'eager' "
+                        "launches each 3 times for rocprofv3")
     p.add_argument("--repack", action="store_true",
                    help="the transpose variants' operand copy at the config-5 shapes: torch's strided "
                         "copy (the reference's .contiguous()) next to pcamd_repack_fp8 (one JSON line)")
@@ -869,6 +873,77 @@ def gemm_ref(torch, dev, steps, warmup, eager):
                                   "layouts, contiguous along the reduction (what torch._scaled_mm takes)"}))
 
 
+# The per-tensor fp8 BMM shapes the reference publishes timings for, (B, M,
+# N, K), B's layout, and the published best time in ms (Triton config sweeps
+# on unstated NVIDIA hardware, fp16 C + fp16 bias; xuOAO/practice_cuda
+# kernels/fp8_bmm/bench/fp8_quant_bmm_best.json:9-1045 for N-major B,
+# fp8_quant_bmm_best_k_order.json:9-1119 for K-major B). Context, not targets.
+PUBLISHED_BMM = [
+    (16, 512, 960, 1280, "n", 0.1461), (16, 2048, 640, 1280, "n", 0.3532), (16, 2048, 1280, 1280, "n", 0.6807),
+    (16, 2048, 1280, 960, "n", 0.5803), (32, 2048, 640, 1280, "n", 0.6987), (32, 2048, 960, 1600, "n", 1.2715),
+    (32, 2048, 1280, 1600, "n", 1.7056), (32, 2048, 1600, 1600, "n", 2.1081), (32, 2048, 1280, 960, "n", 1.1478),
+    (80, 512, 640, 1280, "n", 0.4437), (80, 2048, 640, 640, "n", 1.0126), (80, 2048, 960, 640, "n", 1.4863),
+    (80, 2048, 1280, 640, "n", 1.9913), (80, 2048, 1280, 960, "n", 2.8504), (80, 2048, 640, 1280, "n", 1.7068),
+    (80, 512, 1280, 960, "k", 0.3642), (80, 512, 1280, 640, "k", 0.2535), (80, 512, 960, 640, "k", 0.1935),
+    (32, 512, 1280, 960, "k", 0.1524), (32, 512, 1280, 1600, "k", 0.2462), (32, 512, 960, 1600, "k", 0.1881),
+    (16, 512, 1280, 160, "k", 0.0332), (16, 512, 1280, 960, "k", 0.0803), (16, 512, 1280, 1280, "k", 0.1033),
+    (16, 512, 960, 1280, "k", 0.0800), (80, 512, 80, 640, "k", 0.0353), (16, 512, 160, 1280, "k", 0.0231),
+    (80, 512, 640, 1280, "k", 0.2481), (32, 512, 640, 1280, "k", 0.1034), (16, 512, 640, 1280, "k", 0.0575),
+    (512, 512, 512, 512, "k", 0.5420),
+]
+
+
+def published_bmm(torch, dev, steps, warmup, eager):
+    """The legacy per-tensor BMM (C = (A @ B) * s + bias, fp16 C, fp16 bias
+    [B, M, N]: the signature of the reference's sweep,
+    kernels/fp8_bmm/bench/find_fp8_bmm_best.py:34-53) on PUBLISHED_BMM, with
+    preallocated outputs and enough rotating input sets to exceed the MALL."""
+    from practice_cuda_amd import _lib
+    from practice_cuda_amd.impls import _common as C
+    f8 = torch.float8_e4m3fn
+    g = torch.Generator(device=dev).manual_seed(0)
+    rows = []
+    for bsz, m, n, k, lay, ref_ms in PUBLISHED_BMM:
+        nbytes = bsz * (m * k + k * n + 4 * m * n)  # A, B fp8; bias, C fp16
+        nsets = 1 if eager else max(1, min(8, -(-(512 << 20) // nbytes)))
+        sets = []
+        for _ in range(nsets):
+            a = torch.randn(bsz, m, k, generator=g, device=dev).to(f8)
+            if lay == "n":
+                b = torch.randn(bsz, k, n, generator=g, device=dev).to(f8)
+            else:
+                b = torch.randn(bsz, n, k, generator=g, device=dev).to(f8).transpose(1, 2)
+            bias = torch.randn(bsz, m, n, generator=g, device=dev).half()
+            out = torch.empty(bsz, m, n, device=dev, dtype=torch.float16)
+            sets.append((a, b, bias, out))
+        scale = torch.ones(1, device=dev, dtype=torch.float32)
+
+        def launch(i, sets=sets, scale=scale, bsz=bsz, m=m, n=n, k=k):
+            a, b, bias, out = sets[i % len(sets)]
+            C.launch_bmm(a, b, out, bias, tuple(bias.stride()), _lib.dtype_code(bias.dtype), scale, (0, 0, 0),
+                         None, (0, 0, 0), _lib.SCALE_TENSOR, False, 1, 128, 1, "none", bsz, m, n, k)
+
+        flops = 2 * bsz * m * n * k
+        if eager:
+            for i in range(3):
+                launch(i)
+            torch.cuda.synchronize()
+            continue
+        ms, _ = graph_time(torch, launch, steps, warmup)
+        rows.append({"shape": [bsz, m, n, k], "b_layout": lay, "ms": round(ms, 5),
+                     "TFLOP/s": round(flops / ms / 1e9, 1), "GB/s": round(nbytes / ms / 1e6, 1),
+                     "frac_of_fp8_peak": round(flops / ms / 1e9 / FP8_PEAK_TFLOPS, 4),
+                     "frac_of_hbm_peak": round(nbytes / ms / 1e6 / HBM_PEAK_GBS, 4),
+                     "published_ms": ref_ms, "published_TFLOP/s": round(flops / ref_ms / 1e9, 1),
+                     "rotating_sets": nsets})
+        del sets
+        torch.cuda.empty_cache()
+    if not eager:
+        print(json.dumps({"published_bmm": rows, "what": "per-tensor fp8 e4m3 BMM, fp16 C + fp16 bias [B,M,N], "
+                          "graph-timed median of 5 replays; published_* = the reference's Triton sweep on "
+                          "unstated hardware (context, not a target)"}))
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -896,6 +971,9 @@ def main():
         return
     if args.repack:
         repack_probe(torch, dev, args.steps, args.warmup)
+        return
+    if args.published:
+        published_bmm(torch, dev, args.steps, args.warmup, args.published == "eager")
         return
 
     x2 = make_config2(torch)

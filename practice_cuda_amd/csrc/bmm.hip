@@ -517,17 +517,23 @@ extern "C" int pcamd_bmm_scaled(const void* a, const void* b, int ab_dtype, int6
     return e && e[0] == '0';
   }();
   {
-    const bool wide = k >= 256 && (scale_mode != PCAMD_SCALE_BLOCK || args.qbk == 128) && !env_no_wide;
+    // K not a multiple of 128: the wide kernel masks its last K step (two
+    // steps or more, K a multiple of 4); the other fast kernels need whole steps
+    const bool ragged = k % 128 != 0;
+    const bool wide = k > 128 && (!ragged || k % 4 == 0) &&
+                      (scale_mode != PCAMD_SCALE_BLOCK || args.qbk == 128) && !env_no_wide;
     const int64_t TM = wide ? bmm_wide_tile() : bmm_fast_tile_m();
     const int64_t TN = wide ? bmm_wide_tile() : bmm_fast_tile_n();
     const int64_t tm = (m + TM - 1) / TM, tn = (n + TN - 1) / TN;
     const int64_t lda = a_k ? sam : sak, ldb = b_k ? sbn : sbk;
-    // largest byte offset a workgroup can form (rows padded to the tile)
-    const int64_t a_max = a_k ? (tm * TM) * lda + k : (k - 1) * lda + tm * TM;
-    const int64_t b_max = b_k ? (tn * TN) * ldb + k : (k - 1) * ldb + tn * TN;
+    // largest byte offset a workgroup can form (rows padded to the tile, K to
+    // the step)
+    const int64_t kpad = (k + 127) / 128 * 128;
+    const int64_t a_max = a_k ? (tm * TM) * lda + kpad : (kpad - 1) * lda + tm * TM;
+    const int64_t b_max = b_k ? (tn * TN) * ldb + kpad : (kpad - 1) * ldb + tn * TN;
     const bool block_ok = scale_mode != PCAMD_SCALE_BLOCK ||
                           (args.qbm_shift >= 0 && args.qbn_shift >= 0);
-    const bool fast = k > 0 && k % 128 == 0 && args.vec_a && args.vec_b && lda % 16 == 0 && ldb % 16 == 0 &&
+    const bool fast = k > 0 && (!ragged || wide) && args.vec_a && args.vec_b && lda % 16 == 0 && ldb % 16 == 0 &&
                       a_max < (int64_t{1} << 32) - 64 && b_max < (int64_t{1} << 32) - 64 &&
                       m < INT32_MAX && n < INT32_MAX && k < INT32_MAX && tm * tn * batch < INT32_MAX &&
                       block_ok && !env_generic;
@@ -552,7 +558,7 @@ extern "C" int pcamd_bmm_scaled(const void* a, const void* b, int ab_dtype, int6
       const bool qb1 = scale_mode == PCAMD_SCALE_BLOCK && args.qbk == 128;
       if (!env_no_stream && bmm_stream_ok(f, a_k, b_k, fmode, batch, args.qbm, args.qbn, ssa1, ssb2))
         return bmm_stream_launch(f, ab_dtype, batch, st);
-      if (wide) return bmm_wide_launch(f, ab_dtype, a_k, b_k, fmode, st);
+      if (wide) return bmm_wide_launch(f, ab_dtype, ab_dtype, a_k, b_k, fmode, st);
       return bmm_fast_launch(f, ab_dtype, a_k, b_k, fmode, sb_col, qb1, st);
     }
   }

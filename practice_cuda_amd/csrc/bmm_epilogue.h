@@ -1,4 +1,4 @@
-// bmm_epilogue.h - LDS-staged bf16 output of one wave's 64 x 128 sub-tile.
+// bmm_epilogue.h - LDS-staged 16-bit (bf16 / fp16) output of one wave's 64 x 128 sub-tile.
 //
 // With the MFMA operands swapped, a lane holds 4 consecutive columns of one
 // row per 16 x 16 tile, so direct stores write 32-byte pieces of 16 rows per
@@ -25,22 +25,39 @@ PCAMD_DEV uint32_t pack_bf16_pair(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{lo, hi}, bf16x2));
 }
 
-// Whether the staged path applies: bf16 output without bias or activation,
-// 16-byte aligned rows and N a multiple of 8 (a lane's 8 columns never
-// straddle N).
-PCAMD_DEV bool staged_output_ok(const void* c, int64_t scb, int64_t scm, int n, bool plain) {
-  return plain && (n & 7) == 0 && (scm & 7) == 0 && (scb & 7) == 0 && (reinterpret_cast<uintptr_t>(c) & 15) == 0;
+// Two floats to fp16 (round to nearest even), lo in the low half.
+PCAMD_DEV uint32_t pack_f16_pair(float lo, float hi) {
+  typedef float f32x2 __attribute__((ext_vector_type(2)));
+  typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{lo, hi}, f16x2));
 }
 
-// stg: 8 KiB of LDS private to this wave. c: the batch's C (bf16, row pitch
-// scm elements). The sub-tile covers rows row0 .. row0 + 63 and columns
+// 16-bit output element: bf16 or fp16 (the dtype codes of fp8_common.h), or
+// OUT16_RUNTIME: the one picked by out_f16 at run time
+constexpr int OUT16_RUNTIME = -1;
+template <int OUT>
+PCAMD_DEV uint32_t pack16_pair(float lo, float hi, bool out_f16 = false) {
+  if constexpr (OUT == kF16) return pack_f16_pair(lo, hi);
+  else if constexpr (OUT == kBF16) return pack_bf16_pair(lo, hi);
+  else return out_f16 ? pack_f16_pair(lo, hi) : pack_bf16_pair(lo, hi);
+}
+
+// Whether the staged path applies: a 16-bit output (bf16 or fp16), 16-byte
+// aligned rows and N a multiple of 8 (a lane's 8 columns never straddle N).
+// Bias is applied by the caller's value function.
+PCAMD_DEV bool staged_output_ok(const void* c, int64_t scb, int64_t scm, int n, bool out16) {
+  return out16 && (n & 7) == 0 && (scm & 7) == 0 && (scb & 7) == 0 && (reinterpret_cast<uintptr_t>(c) & 15) == 0;
+}
+
+// stg: 8 KiB of LDS private to this wave. c: the batch's C (OUT elements, row
+// pitch scm elements). The sub-tile covers rows row0 .. row0 + 63 and columns
 // col0 .. col0 + 127; value(i, j, v) fills the 4 outputs of this lane in
 // MFMA tile (i, j): row row0 + 16 i + (lane & 15), columns
 // col0 + 16 j + 4 (lane >> 4) + r. The sub-tile goes out in two halves of
 // 32 rows; staged chunk c of row r sits at LDS position c ^ (r & 15).
-template <typename ValueFn>
-PCAMD_DEV void store_subtile_staged(uint8_t* stg, __bf16* c, int64_t scm, int m, int n, int row0, int col0,
-                                    int lane, ValueFn&& value) {
+template <int OUT = kBF16, typename ValueFn>
+PCAMD_DEV void store_subtile_staged(uint8_t* stg, uint16_t* c, int64_t scm, int m, int n, int row0, int col0,
+                                    int lane, ValueFn&& value, bool out_f16 = false) {
   typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
   const int lr = lane & 15, lg = lane >> 4;
 #pragma unroll
@@ -54,7 +71,7 @@ PCAMD_DEV void store_subtile_staged(uint8_t* stg, __bf16* c, int64_t scm, int m,
         const int r = 16 * il + lr;
         const int chunk = 2 * j + (lg >> 1);
         uint2* dst = reinterpret_cast<uint2*>(stg + r * 256 + ((chunk ^ (r & 15)) << 4) + ((lg & 1) << 3));
-        *dst = make_uint2(pack_bf16_pair(v[0], v[1]), pack_bf16_pair(v[2], v[3]));
+        *dst = make_uint2(pack16_pair<OUT>(v[0], v[1], out_f16), pack16_pair<OUT>(v[2], v[3], out_f16));
       }
     }
     // LDS operations of one wave complete in order; the wait keeps the
@@ -79,9 +96,9 @@ PCAMD_DEV void store_subtile_staged(uint8_t* stg, __bf16* c, int64_t scm, int m,
 // row0 + 16 i + (lane & 15), columns col0 + 16 jj + 4 (lane >> 4) + r. Two
 // pieces of 32 rows; staged chunk c of row r sits at LDS position c ^ (r & 7).
 // Each store instruction writes 8 rows x 128 contiguous bytes.
-template <typename ValueFn>
-PCAMD_DEV void store_half_staged(uint8_t* stg, __bf16* c, int64_t scm, int m, int n, int row0, int col0, int lane,
-                                 ValueFn&& value) {
+template <int OUT = kBF16, typename ValueFn>
+PCAMD_DEV void store_half_staged(uint8_t* stg, uint16_t* c, int64_t scm, int m, int n, int row0, int col0, int lane,
+                                 ValueFn&& value, bool out_f16 = false) {
   typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
   const int lr = lane & 15, lg = lane >> 4;
 #pragma unroll
@@ -95,7 +112,7 @@ PCAMD_DEV void store_half_staged(uint8_t* stg, __bf16* c, int64_t scm, int m, in
         const int r = 16 * il + lr;
         const int chunk = 2 * jj + (lg >> 1);
         uint2* dst = reinterpret_cast<uint2*>(stg + r * 128 + ((chunk ^ (r & 7)) << 4) + ((lg & 1) << 3));
-        *dst = make_uint2(pack_bf16_pair(v[0], v[1]), pack_bf16_pair(v[2], v[3]));
+        *dst = make_uint2(pack16_pair<OUT>(v[0], v[1], out_f16), pack16_pair<OUT>(v[2], v[3], out_f16));
       }
     }
     // LDS operations of one wave complete in order; the wait keeps the

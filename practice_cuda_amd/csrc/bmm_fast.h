@@ -57,9 +57,11 @@ bool bmm_stream_ok(const FastArgs& a, bool a_k, bool b_k, int mode, int64_t batc
                    int64_t ssa1, int64_t ssb2);
 int bmm_stream_launch(const FastArgs& a, int ab_dtype, int64_t batch, hipStream_t st);
 
-// 256 x 256-tile, 8-wave kernel for two or more K steps (bmm_wide.hip)
-// block mode requires quant_block_k == 128 and power-of-two qbm / qbn
-int bmm_wide_launch(const FastArgs& a, int ab_dtype, bool a_k, bool b_k, int mode, hipStream_t st);
+// 256 x 256-tile, 8-wave kernel for two or more K steps (bmm_wide.h,
+// bmm_wide*.hip); K a multiple of 4 (a last K step of fewer than 128 is
+// masked); block mode requires quant_block_k == 128 and power-of-two qbm /
+// qbn. a_fmt / b_fmt: the fp8 format of each operand (PCAMD_FP8_*).
+int bmm_wide_launch(const FastArgs& a, int a_fmt, int b_fmt, bool a_k, bool b_k, int mode, hipStream_t st);
 int bmm_wide_tile();
 
 }  // namespace pcamd

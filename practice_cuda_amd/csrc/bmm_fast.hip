@@ -436,7 +436,7 @@ __global__ __launch_bounds__(NT, 1) void bmm_fast_kernel(FastArgs a) {
     if (staged_output_ok(a.c, a.scb, a.scm, a.n, plain)) {
       // the stage the last K step did not read is free (every wave passed the
       // last barrier after its final read of it): 8 KiB of it per wave
-      store_subtile_staged(smem + (ksteps & 1) * STAGE + wave * 8192, reinterpret_cast<__bf16*>(a.c) + bidx * a.scb,
+      store_subtile_staged(smem + (ksteps & 1) * STAGE + wave * 8192, reinterpret_cast<uint16_t*>(a.c) + bidx * a.scb,
                            a.scm, a.m, a.n, m0 + wm * 64, n0 + wn * 128, lane, value);
       return;
     }
@@ -590,7 +590,7 @@ __global__ __launch_bounds__(NT, STAGED ? 3 : 2) void bmm_single_kernel(FastArgs
         }
       };
       if constexpr (STAGED) {
-        store_half_staged(smem + wave * 4096, reinterpret_cast<__bf16*>(a.c) + bidx * a.scb, a.scm, a.m, a.n,
+        store_half_staged(smem + wave * 4096, reinterpret_cast<uint16_t*>(a.c) + bidx * a.scb, a.scm, a.m, a.n,
                           m0 + wm * 64, n0 + wn * 128 + 64 * h, lane, value);
         continue;
       }
