@@ -26,6 +26,11 @@
  *                          impls/triton_per_channel.py:271-427 (channel scales),
  *                          impls/triton_per_tensor.py:140-306 and
  *                          kernels/fp8_bmm/fp8_warper.py:79-129 (tensor scale)
+ *   pcamd_bmm_scaled_mixed <- the same GEMM with an e5m2 and an e4m3fn operand:
+ *                          fp8_training/fp8_bench/modules/bmm_linear.py:121-227
+ *                          (custom op fp8_bench::bmm_linear_tma, called for
+ *                          dgrad / wgrad at :402-410, :441-446 with torchao's
+ *                          e5m2 grad_output and e4m3fn input / weight, :43-46)
  */
 #ifndef PCAMD_FP8_H
 #define PCAMD_FP8_H
@@ -36,7 +41,7 @@
 extern "C" {
 #endif
 
-#define PCAMD_ABI_VERSION 1
+#define PCAMD_ABI_VERSION 2 /* 2: pcamd_bmm_scaled_mixed */
 
 /* status codes */
 #define PCAMD_OK 0
@@ -157,6 +162,26 @@ int pcamd_bmm_scaled(const void *a, const void *b, int ab_dtype,
                      int64_t ssbb, int64_t ssb1, int64_t ssb2, int scale_mode,
                      int scales_are_quant, int64_t qbm, int64_t qbk,
                      int64_t qbn, int activation, void *stream);
+
+/*
+ * pcamd_bmm_scaled with a format code per operand (a_dtype, b_dtype:
+ * PCAMD_E4M3FN or PCAMD_E5M2, equal or not): the training recipe's e5m2
+ * gradient times an e4m3fn weight or activation. Every other argument and
+ * the math are those of pcamd_bmm_scaled, which is this call with a_dtype ==
+ * b_dtype. Available from PCAMD_ABI_VERSION 2.
+ */
+int pcamd_bmm_scaled_mixed(const void *a, int a_dtype, const void *b,
+                           int b_dtype, int64_t batch, int64_t m, int64_t n,
+                           int64_t k, int64_t sab, int64_t sam, int64_t sak,
+                           int64_t sbb, int64_t sbk, int64_t sbn, void *c,
+                           int c_dtype, int64_t scb, int64_t scm, int64_t scn,
+                           const void *bias, int bias_dtype, int64_t sbiasb,
+                           int64_t sbiasm, int64_t sbiasn, const float *sa,
+                           int64_t ssab, int64_t ssa1, int64_t ssa2,
+                           const float *sb, int64_t ssbb, int64_t ssb1,
+                           int64_t ssb2, int scale_mode, int scales_are_quant,
+                           int64_t qbm, int64_t qbk, int64_t qbn,
+                           int activation, void *stream);
 
 /*
  * Block-scaled FP8 GEMM with the activation quantization fused into the K

@@ -40,6 +40,7 @@ EXPORTED_SYMBOLS = (
     "pcamd_quant_channel",
     "pcamd_quant_tensor",
     "pcamd_bmm_scaled",
+    "pcamd_bmm_scaled_mixed",
     "pcamd_bmm_quant_a",
     "pcamd_repack_fp8",
 )
@@ -75,6 +76,11 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.pcamd_bmm_scaled.restype = _int
     lib.pcamd_bmm_scaled.argtypes = (
         [_ptr, _ptr, _int] + [_i64] * 4 + [_i64] * 6 + [_ptr, _int] + [_i64] * 3
+        + [_ptr, _int] + [_i64] * 3 + [_ptr] + [_i64] * 3 + [_ptr] + [_i64] * 3
+        + [_int, _int, _i64, _i64, _i64, _int, _ptr])
+    lib.pcamd_bmm_scaled_mixed.restype = _int
+    lib.pcamd_bmm_scaled_mixed.argtypes = (
+        [_ptr, _int, _ptr, _int] + [_i64] * 4 + [_i64] * 6 + [_ptr, _int] + [_i64] * 3
         + [_ptr, _int] + [_i64] * 3 + [_ptr] + [_i64] * 3 + [_ptr] + [_i64] * 3
         + [_int, _int, _i64, _i64, _i64, _int, _ptr])
     lib.pcamd_bmm_quant_a.restype = _int

@@ -183,10 +183,13 @@ struct Stage<false> {
   }
 };
 
-template <int FMT>
+// Format codes per operand (0 = fp8 e4m3, 1 = bf8 e5m2). The operands are
+// swapped (x: B fragment, y: A fragment), so src0's code (cbsz) is B's and
+// src1's (blgp) is A's.
+template <int FA, int FB>
 PCAMD_DEV v4f mfma(const v8i& x, const v8i& y, const v4f& c) {
-  constexpr int code = FMT == kE5M2 ? 1 : 0;  // 0 = fp8 e4m3, 1 = bf8 e5m2
-  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(x, y, c, code, code, 0, 0, 0, 0);
+  constexpr int ca = FA == kE5M2 ? 1 : 0, cb = FB == kE5M2 ? 1 : 0;
+  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(x, y, c, cb, ca, 0, 0, 0, 0);
 }
 
 PCAMD_DEV int64_t qidx(int64_t v, int32_t shift, int64_t q) { return shift >= 0 ? (v >> shift) : v / q; }
@@ -239,7 +242,7 @@ PCAMD_DEV uint32_t pack_bf16x2(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{lo, hi}, bf16x2));
 }
 
-template <bool A_K, bool B_K, int FMT, int MODE>
+template <bool A_K, bool B_K, int FA, int FB, int MODE>
 __global__ __launch_bounds__(NT) void bmm_kernel(Args a) {
   __shared__ __attribute__((aligned(16))) uint8_t lds_a[BM * BK];
   __shared__ __attribute__((aligned(16))) uint8_t lds_b[BN * BK];
@@ -306,7 +309,7 @@ __global__ __launch_bounds__(NT) void bmm_kernel(Args a) {
       for (int i = 0; i < 4; ++i) {
         const v8i afr = Stage<A_K>::frag(lds_a, wm * 64 + i * 16 + lr, lg);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = mfma<FMT>(bfr[j], afr, acc[i][j]);
+        for (int j = 0; j < 4; ++j) acc[i][j] = mfma<FA, FB>(bfr[j], afr, acc[i][j]);
       }
     } else {
       // block scales: quant-K block of this step and whether it ends here
@@ -336,14 +339,14 @@ __global__ __launch_bounds__(NT) void bmm_kernel(Args a) {
         if constexpr (MODE == kBlock128) {
           v4f p[4];
 #pragma unroll
-          for (int j = 0; j < 4; ++j) p[j] = mfma<FMT>(bfr[j], afr, v4f{0.f, 0.f, 0.f, 0.f});
+          for (int j = 0; j < 4; ++j) p[j] = mfma<FA, FB>(bfr[j], afr, v4f{0.f, 0.f, 0.f, 0.f});
 #pragma unroll
           for (int j = 0; j < 4; ++j)
 #pragma unroll
             for (int r = 0; r < 4; ++r) acc[i][j][r] += p[j][r] * (sav[i] * sbv[j][r]);
         } else {
 #pragma unroll
-          for (int j = 0; j < 4; ++j) part[i][j] = mfma<FMT>(bfr[j], afr, part[i][j]);
+          for (int j = 0; j < 4; ++j) part[i][j] = mfma<FA, FB>(bfr[j], afr, part[i][j]);
           if (block_end) {
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
@@ -405,24 +408,31 @@ __global__ __launch_bounds__(NT) void bmm_kernel(Args a) {
   }
 }
 
-template <bool A_K, bool B_K, int FMT>
+template <bool A_K, bool B_K, int FA, int FB>
 int launch_mode(const Args& a, int mode, hipStream_t st) {
   const int grid = static_cast<int>(a.total_tiles);
   switch (mode) {
-    case kBlock128: bmm_kernel<A_K, B_K, FMT, kBlock128><<<grid, NT, 0, st>>>(a); break;
-    case kBlockWide: bmm_kernel<A_K, B_K, FMT, kBlockWide><<<grid, NT, 0, st>>>(a); break;
-    case kChannel: bmm_kernel<A_K, B_K, FMT, kChannel><<<grid, NT, 0, st>>>(a); break;
-    default: bmm_kernel<A_K, B_K, FMT, kTensor><<<grid, NT, 0, st>>>(a); break;
+    case kBlock128: bmm_kernel<A_K, B_K, FA, FB, kBlock128><<<grid, NT, 0, st>>>(a); break;
+    case kBlockWide: bmm_kernel<A_K, B_K, FA, FB, kBlockWide><<<grid, NT, 0, st>>>(a); break;
+    case kChannel: bmm_kernel<A_K, B_K, FA, FB, kChannel><<<grid, NT, 0, st>>>(a); break;
+    default: bmm_kernel<A_K, B_K, FA, FB, kTensor><<<grid, NT, 0, st>>>(a); break;
   }
   return check_launch("bmm_kernel");
 }
 
-template <int FMT>
+template <int FA, int FB>
 int launch_layout(const Args& a, bool a_k, bool b_k, int mode, hipStream_t st) {
-  if (a_k && b_k) return launch_mode<true, true, FMT>(a, mode, st);
-  if (a_k && !b_k) return launch_mode<true, false, FMT>(a, mode, st);
-  if (!a_k && b_k) return launch_mode<false, true, FMT>(a, mode, st);
-  return launch_mode<false, false, FMT>(a, mode, st);
+  if (a_k && b_k) return launch_mode<true, true, FA, FB>(a, mode, st);
+  if (a_k && !b_k) return launch_mode<true, false, FA, FB>(a, mode, st);
+  if (!a_k && b_k) return launch_mode<false, true, FA, FB>(a, mode, st);
+  return launch_mode<false, false, FA, FB>(a, mode, st);
+}
+
+inline int launch_formats(const Args& a, int a_fmt, int b_fmt, bool a_k, bool b_k, int mode, hipStream_t st) {
+  if (a_fmt == kE4M3 && b_fmt == kE4M3) return launch_layout<kE4M3, kE4M3>(a, a_k, b_k, mode, st);
+  if (a_fmt == kE5M2 && b_fmt == kE5M2) return launch_layout<kE5M2, kE5M2>(a, a_k, b_k, mode, st);
+  if (a_fmt == kE5M2) return launch_layout<kE5M2, kE4M3>(a, a_k, b_k, mode, st);
+  return launch_layout<kE4M3, kE5M2>(a, a_k, b_k, mode, st);
 }
 
 inline int log2_or_neg(int64_t v) {
@@ -437,18 +447,20 @@ inline int log2_or_neg(int64_t v) {
 
 using namespace pcamd;
 
-extern "C" int pcamd_bmm_scaled(const void* a, const void* b, int ab_dtype, int64_t batch, int64_t m,
-                                int64_t n, int64_t k, int64_t sab, int64_t sam, int64_t sak,
-                                int64_t sbb, int64_t sbk, int64_t sbn, void* c, int c_dtype,
-                                int64_t scb, int64_t scm, int64_t scn, const void* bias,
-                                int bias_dtype, int64_t sbiasb, int64_t sbiasm, int64_t sbiasn,
-                                const float* sa, int64_t ssab, int64_t ssa1, int64_t ssa2,
-                                const float* sb, int64_t ssbb, int64_t ssb1, int64_t ssb2,
-                                int scale_mode, int scales_are_quant, int64_t qbm, int64_t qbk,
-                                int64_t qbn, int activation, void* stream) {
-  clear_error();
-  if (ab_dtype != kE4M3 && ab_dtype != kE5M2)
-    return set_error(PCAMD_ERR_INVALID, "a/b must be fp8 (code %d or %d), got %d", kE4M3, kE5M2, ab_dtype);
+// The body of pcamd_bmm_scaled and pcamd_bmm_scaled_mixed: a_fmt / b_fmt
+// are each operand's fp8 format.
+static int bmm_scaled(const void* a, int a_fmt, const void* b, int b_fmt, int64_t batch, int64_t m, int64_t n,
+                      int64_t k, int64_t sab, int64_t sam, int64_t sak, int64_t sbb, int64_t sbk, int64_t sbn,
+                      void* c, int c_dtype, int64_t scb, int64_t scm, int64_t scn, const void* bias,
+                      int bias_dtype, int64_t sbiasb, int64_t sbiasm, int64_t sbiasn, const float* sa,
+                      int64_t ssab, int64_t ssa1, int64_t ssa2, const float* sb, int64_t ssbb, int64_t ssb1,
+                      int64_t ssb2, int scale_mode, int scales_are_quant, int64_t qbm, int64_t qbk, int64_t qbn,
+                      int activation, void* stream) {
+  if (a_fmt != kE4M3 && a_fmt != kE5M2)
+    return set_error(PCAMD_ERR_INVALID, "a must be fp8 (code %d or %d), got %d", kE4M3, kE5M2, a_fmt);
+  if (b_fmt != kE4M3 && b_fmt != kE5M2)
+    return set_error(PCAMD_ERR_INVALID, "b must be fp8 (code %d or %d), got %d", kE4M3, kE5M2, b_fmt);
+  const bool same_fmt = a_fmt == b_fmt;
   if (c_dtype != kF32 && c_dtype != kBF16 && c_dtype != kF16 && c_dtype != kE4M3 && c_dtype != kE5M2)
     return set_error(PCAMD_ERR_INVALID, "unsupported output dtype code %d", c_dtype);
   if (bias && bias_dtype != kF32 && bias_dtype != kBF16 && bias_dtype != kF16)
@@ -556,14 +568,43 @@ extern "C" int pcamd_bmm_scaled(const void* a, const void* b, int ab_dtype, int6
       const int fmode = scale_mode == PCAMD_SCALE_BLOCK ? 0 : scale_mode == PCAMD_SCALE_CHANNEL ? 1 : 2;
       const bool sb_col = scale_mode == PCAMD_SCALE_BLOCK && args.qbn < 16;
       const bool qb1 = scale_mode == PCAMD_SCALE_BLOCK && args.qbk == 128;
-      if (!env_no_stream && bmm_stream_ok(f, a_k, b_k, fmode, batch, args.qbm, args.qbn, ssa1, ssb2))
-        return bmm_stream_launch(f, ab_dtype, batch, st);
-      if (wide) return bmm_wide_launch(f, ab_dtype, ab_dtype, a_k, b_k, fmode, st);
-      return bmm_fast_launch(f, ab_dtype, a_k, b_k, fmode, sb_col, qb1, st);
+      // the streaming (config-4) and 128 x 256 kernels take one format for both operands
+      if (same_fmt && !env_no_stream && bmm_stream_ok(f, a_k, b_k, fmode, batch, args.qbm, args.qbn, ssa1, ssb2))
+        return bmm_stream_launch(f, a_fmt, batch, st);
+      if (wide) return bmm_wide_launch(f, a_fmt, b_fmt, a_k, b_k, fmode, st);
+      if (same_fmt) return bmm_fast_launch(f, a_fmt, a_k, b_k, fmode, sb_col, qb1, st);
     }
   }
-  if (ab_dtype == kE5M2) return bmm::launch_layout<kE5M2>(args, a_k, b_k, mode, st);
-  return bmm::launch_layout<kE4M3>(args, a_k, b_k, mode, st);
+  return bmm::launch_formats(args, a_fmt, b_fmt, a_k, b_k, mode, st);
+}
+
+extern "C" int pcamd_bmm_scaled(const void* a, const void* b, int ab_dtype, int64_t batch, int64_t m,
+                                int64_t n, int64_t k, int64_t sab, int64_t sam, int64_t sak,
+                                int64_t sbb, int64_t sbk, int64_t sbn, void* c, int c_dtype,
+                                int64_t scb, int64_t scm, int64_t scn, const void* bias,
+                                int bias_dtype, int64_t sbiasb, int64_t sbiasm, int64_t sbiasn,
+                                const float* sa, int64_t ssab, int64_t ssa1, int64_t ssa2,
+                                const float* sb, int64_t ssbb, int64_t ssb1, int64_t ssb2,
+                                int scale_mode, int scales_are_quant, int64_t qbm, int64_t qbk,
+                                int64_t qbn, int activation, void* stream) {
+  clear_error();
+  return bmm_scaled(a, ab_dtype, b, ab_dtype, batch, m, n, k, sab, sam, sak, sbb, sbk, sbn, c, c_dtype, scb, scm,
+                    scn, bias, bias_dtype, sbiasb, sbiasm, sbiasn, sa, ssab, ssa1, ssa2, sb, ssbb, ssb1, ssb2,
+                    scale_mode, scales_are_quant, qbm, qbk, qbn, activation, stream);
+}
+
+extern "C" int pcamd_bmm_scaled_mixed(const void* a, int a_dtype, const void* b, int b_dtype, int64_t batch,
+                                      int64_t m, int64_t n, int64_t k, int64_t sab, int64_t sam, int64_t sak,
+                                      int64_t sbb, int64_t sbk, int64_t sbn, void* c, int c_dtype, int64_t scb,
+                                      int64_t scm, int64_t scn, const void* bias, int bias_dtype, int64_t sbiasb,
+                                      int64_t sbiasm, int64_t sbiasn, const float* sa, int64_t ssab, int64_t ssa1,
+                                      int64_t ssa2, const float* sb, int64_t ssbb, int64_t ssb1, int64_t ssb2,
+                                      int scale_mode, int scales_are_quant, int64_t qbm, int64_t qbk, int64_t qbn,
+                                      int activation, void* stream) {
+  clear_error();
+  return bmm_scaled(a, a_dtype, b, b_dtype, batch, m, n, k, sab, sam, sak, sbb, sbk, sbn, c, c_dtype, scb, scm, scn,
+                    bias, bias_dtype, sbiasb, sbiasm, sbiasn, sa, ssab, ssa1, ssa2, sb, ssbb, ssb1, ssb2, scale_mode,
+                    scales_are_quant, qbm, qbk, qbn, activation, stream);
 }
 
 // Block-scaled BMM with the A operand quantized inside the kernel (1 x 128

@@ -201,9 +201,15 @@ def launch_bmm(a_tensor, b_tensor, out, bias, bias_strides, bias_code, sa, sa_st
                batch, m, n, k) -> torch.Tensor:
     _lib.require_gpu_tensor(a_tensor, "A")
     L = _lib.lib()
+    # one fp8 format for both operands (the registry wrappers' contract), or
+    # one each (the training layer's e5m2 gradient times an e4m3 operand)
+    fmt = ((_lib.dtype_code(a_tensor.dtype),) if a_tensor.dtype == b_tensor.dtype
+           else (_lib.dtype_code(a_tensor.dtype), _lib.dtype_code(b_tensor.dtype)))
+    entry = L.pcamd_bmm_scaled if len(fmt) == 1 else L.pcamd_bmm_scaled_mixed
     with torch.cuda.device(a_tensor.device):
-        rc = L.pcamd_bmm_scaled(
-            _lib.ptr(a_tensor), _lib.ptr(b_tensor), _lib.dtype_code(a_tensor.dtype),
+        rc = entry(
+            *((_lib.ptr(a_tensor), _lib.ptr(b_tensor), fmt[0]) if len(fmt) == 1
+              else (_lib.ptr(a_tensor), fmt[0], _lib.ptr(b_tensor), fmt[1])),
             batch, m, n, k,
             *a_tensor.stride(), *b_tensor.stride(),
             _lib.ptr(out), _lib.dtype_code(out.dtype), *out.stride(),
@@ -212,5 +218,5 @@ def launch_bmm(a_tensor, b_tensor, out, bias, bias_strides, bias_code, sa, sa_st
             scale_mode, int(scales_are_quant), qbm, qbk, qbn,
             _lib.ACT_GELU if activation == "gelu" else _lib.ACT_NONE,
             _lib.stream_of(a_tensor))
-    _lib.check(rc, "pcamd_bmm_scaled")
+    _lib.check(rc, "pcamd_bmm_scaled" if len(fmt) == 1 else "pcamd_bmm_scaled_mixed")
     return out

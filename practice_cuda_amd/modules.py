@@ -58,7 +58,9 @@ def block_scaled_bmm(
     """``C[b] = sum_kq (A[b, :, kq] @ B[b, kq, :]) * sa[b, m/qbm, kq] * sb[b, kq, n/qbn] (+ bias)``.
 
     a: fp8 [B, M, K] contiguous along K or M; b: fp8 [B, K, N] contiguous
-    along N or K; sa: fp32 [B, ceil(M/qbm), ceil(K/qbk)]; sb: fp32
+    along N or K (each e4m3fn or e5m2, the same or not: the recipe's e5m2
+    gradient times an e4m3fn weight or activation); sa: fp32
+    [B, ceil(M/qbm), ceil(K/qbk)]; sb: fp32
     [B, ceil(K/qbk), ceil(N/qbn)] (any strides); bias: [B, N] (broadcast over
     M) or None. qbk must be a multiple of 128; a last, partial K block is
     scaled like the others (its quantization covered the same columns).
@@ -67,8 +69,8 @@ def block_scaled_bmm(
     n = b.shape[2]
     if b.shape[0] != batch or b.shape[1] != k:
         raise ValueError(f"incompatible BMM shapes: A={tuple(a.shape)}, B={tuple(b.shape)}")
-    if a.dtype not in _FP8 or b.dtype != a.dtype:
-        raise ValueError(f"A and B must share an fp8 dtype, got {a.dtype} and {b.dtype}")
+    if a.dtype not in _FP8 or b.dtype not in _FP8:
+        raise ValueError(f"A and B must be fp8 (e4m3fn or e5m2), got {a.dtype} and {b.dtype}")
     if qbk <= 0 or qbk % 128:
         raise ValueError(f"quant block K ({qbk}) must be a positive multiple of 128")
     want_a = (batch, -(-m // qbm), -(-k // qbk))
@@ -175,20 +177,28 @@ class Float8BlockBMMLinearConfig:
 
     granularity "block": 1x128 activations / gradients, 128x128 weights, 128x1
     re-quantization for wgrad (quant block 128). "tensor": one scale per
-    tensor. fp8_dtype applies to every operand (the GEMM needs one fp8 format
-    per call); eps is the amax floor of the quantizers.
+    tensor. fp8_dtype is the format of the input and the weight;
+    grad_fp8_dtype that of the gradient dY (None: fp8_dtype, the block
+    recipe's e4m3fn everywhere; torch.float8_e5m2: torchao's default for
+    grad_output, which the reference layer keeps,
+    fp8_training/fp8_bench/modules/bmm_linear.py:43-46 - dgrad and wgrad then
+    multiply e5m2 by e4m3fn). eps is the amax floor of the quantizers.
     """
 
     granularity: str = "block"
     fp8_dtype: torch.dtype = torch.float8_e4m3fn
     block: int = 128
     eps: float = 1e-12
+    grad_fp8_dtype: Optional[torch.dtype] = None
 
     def __post_init__(self) -> None:
         if self.granularity not in ("block", "tensor"):
             raise ValueError(f"granularity must be 'block' or 'tensor', got {self.granularity!r}")
         if self.fp8_dtype not in _FP8:
             raise ValueError(f"fp8_dtype must be float8_e4m3fn or float8_e5m2, got {self.fp8_dtype}")
+        if self.grad_fp8_dtype is not None and self.grad_fp8_dtype not in _FP8:
+            raise ValueError("grad_fp8_dtype must be float8_e4m3fn, float8_e5m2 or None, "
+                             f"got {self.grad_fp8_dtype}")
         if self.block != 128:
             raise ValueError("the block recipe uses 128-wide quant blocks")
 
@@ -226,7 +236,8 @@ class _Float8BlockBMMLinearFunction(torch.autograd.Function):
     @staticmethod
     def backward(ctx, grad_output: torch.Tensor):
         config = ctx.config
-        f8, eps, blk = config.fp8_dtype, config.eps, config.block
+        eps, blk = config.eps, config.block
+        f8 = config.grad_fp8_dtype or config.fp8_dtype  # dY's format
         dy = grad_output.contiguous()
         grad_input = grad_weight = grad_bias = None
         if config.granularity == "tensor":
@@ -330,7 +341,7 @@ class Float8BMMLinear(BMMLinear):
 
     def extra_repr(self) -> str:
         return (super().extra_repr() + f", granularity={self.config.granularity}, "
-                f"fp8_dtype={self.config.fp8_dtype}")
+                f"fp8_dtype={self.config.fp8_dtype}, grad_fp8_dtype={self.config.grad_fp8_dtype}")
 
     @classmethod
     def from_float(cls, module: BMMLinear,

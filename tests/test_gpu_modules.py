@@ -70,6 +70,58 @@ def test_block_recipe_gemms_match_oracle(dev, shape):
     assert y.dtype == dx.dtype == dw.dtype == torch.bfloat16
 
 
+@pytest.mark.parametrize("shape", [(2, 256, 384, 512), (1, 130, 200, 256), (1, 512, 640, 960)])
+def test_block_recipe_e5m2_grads_match_oracle(dev, shape):
+    """grad_fp8_dtype = e5m2 (torchao's grad_output format, kept by the
+    reference layer, fp8_training/fp8_bench/modules/bmm_linear.py:43-46):
+    dgrad multiplies e5m2 dY (1x128) by e4m3 W (128x128) and wgrad e5m2 dY
+    (128x1) by e4m3 X (128x1), each against the fp64 product of the oracle's
+    quantizations in those formats; the forward stays e4m3 x e4m3."""
+    b, m, k, n = shape
+    print(f"block recipe e5m2 grads {shape}", flush=True)
+    cfg = Float8BlockBMMLinearConfig(grad_fp8_dtype=torch.float8_e5m2)
+    layer = _layer(b, k, n, dev, cfg)
+    g = torch.Generator().manual_seed(4)
+    x = torch.randn(b, m, k, generator=g).bfloat16()
+    dy = (torch.randn(b, m, n, generator=g) * 1e-3).bfloat16()
+    y, dx, dw, _ = _run(layer, x, dy, dev)
+    w = layer.weight.detach().cpu()
+
+    def deq(t, bm, bn, fmt):
+        q, sc = O.quant_block(t.cpu(), bm, bn, fmt=fmt)
+        return O.dequant_block(q, sc, bm, bn, fmt=fmt)
+
+    y_ref = np.matmul(deq(x, 1, 128, "e4m3"), np.swapaxes(deq(w, 128, 128, "e4m3"), -1, -2))
+    y_ref = y_ref + layer.bias.detach().cpu().double().numpy()[:, None, :]
+    dx_ref = np.matmul(deq(dy, 1, 128, "e5m2"), deq(w, 128, 128, "e4m3"))
+    dw_ref = np.matmul(np.swapaxes(deq(dy, 128, 1, "e5m2"), -1, -2), deq(x, 128, 1, "e4m3"))
+    assert O.max_abs_rel(y.float().cpu().numpy(), y_ref) <= 1e-2
+    assert O.max_abs_rel(dx.float().cpu().numpy(), dx_ref) <= 1e-2
+    assert O.max_abs_rel(dw.float().cpu().numpy(), dw_ref) <= 1e-2
+    # and the e5m2 gradient is not the e4m3 one: the formats differ in the products
+    dx4 = np.matmul(deq(dy, 1, 128, "e4m3"), deq(w, 128, 128, "e4m3"))
+    assert not np.array_equal(dx_ref, dx4)
+
+
+def test_tensor_recipe_e5m2_grads_match_oracle(dev):
+    b, m, k, n = 2, 96, 160, 200
+    cfg = Float8BlockBMMLinearConfig(granularity="tensor", grad_fp8_dtype=torch.float8_e5m2)
+    layer = _layer(b, k, n, dev, cfg, bias=False)
+    g = torch.Generator().manual_seed(5)
+    x = torch.randn(b, m, k, generator=g).bfloat16()
+    dy = torch.randn(b, m, n, generator=g).bfloat16()
+    y, dx, dw, _ = _run(layer, x, dy, dev)
+    w = layer.weight.detach().cpu()
+
+    def deq(t, fmt):
+        q, ds, _ = O.quant_tensor(t.cpu(), fmt)
+        return O.decode(q, fmt).astype(np.float64) * np.float64(ds)
+
+    assert O.max_abs_rel(dx.float().cpu().numpy(), np.matmul(deq(dy, "e5m2"), deq(w, "e4m3"))) <= 1e-2
+    assert O.max_abs_rel(dw.float().cpu().numpy(),
+                         np.matmul(np.swapaxes(deq(dy, "e5m2"), -1, -2), deq(x, "e4m3"))) <= 1e-2
+
+
 def test_tensor_recipe_gemms_match_oracle(dev):
     b, m, k, n = 2, 96, 160, 200
     layer = _layer(b, k, n, dev, Float8BlockBMMLinearConfig(granularity="tensor"), bias=False)

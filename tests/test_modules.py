@@ -24,6 +24,9 @@ def test_config_validation():
         Float8BlockBMMLinearConfig(fp8_dtype=torch.bfloat16)
     with pytest.raises(ValueError, match="128"):
         Float8BlockBMMLinearConfig(block=64)
+    with pytest.raises(ValueError, match="grad_fp8_dtype"):
+        Float8BlockBMMLinearConfig(grad_fp8_dtype=torch.float16)
+    assert Float8BlockBMMLinearConfig(grad_fp8_dtype=torch.float8_e5m2).grad_fp8_dtype == torch.float8_e5m2
 
 
 def test_bmm_linear_baseline_and_errors():

@@ -148,6 +148,12 @@ def test_bmm_validation_errors():
         hip_per_block_bmm(a, b, bias=torch.zeros(2, 64, 95))
     with pytest.raises(ValueError, match="GPU tensor"):
         hip_per_block_bmm(a, b)
+    # the registry wrappers keep the reference's one-format rule
+    # (impls/triton_per_block.py:288-290); mixed formats are the training
+    # layer's (pcamd::block_scaled_bmm over pcamd_bmm_scaled_mixed)
+    b5 = R.QuantResult(b.tensor.to(torch.float8_e5m2), b.dequant_scale, "t", "block", blk(128, 128))
+    with pytest.raises(ValueError, match="same FP8 dtype"):
+        hip_per_block_bmm(a, b5)
     ca = _qr((2, 64, 256), "channel", {"channel_axis": -2}, (2, 64))
     cb = _qr((2, 256, 96), "channel", {"channel_axis": -2}, (2, 96))
     with pytest.raises(ValueError, match="channel_axis=-1"):
