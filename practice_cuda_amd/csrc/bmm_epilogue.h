@@ -131,4 +131,56 @@ PCAMD_DEV void store_half_staged(uint8_t* stg, uint16_t* c, int64_t scm, int m, 
   }
 }
 
+// Transposed output of one wave's 64 x (16 * JN) sub-tile: the kernel
+// computed C' = B^T A^T, and C (the caller's) holds its transpose, so the
+// lane's 4 consecutive n' of one m' go to 4 rows of C at one column. stg: 16
+// KiB of LDS private to this wave, laid out as the wave's block of C: staged
+// row R = n' - col0 (16 * JN rows), 64 m' per row (128 bytes), 16-byte chunk
+// q of row R at position q ^ (R & 7). Lanes pair up (lane ^ 1 holds the next
+// m'): each lane of a pair writes one dword (two m') to two of the four rows,
+// after one DPP swap. Each store instruction then writes 8 rows x 128
+// contiguous bytes of C. c: the batch's C, row pitch ld elements; rows n' <
+// n and columns m' < m are stored (m a multiple of 8).
+template <int OUT, int JN, typename ValueFn>
+PCAMD_DEV void store_subtile_staged_t(uint8_t* stg, uint16_t* c, int64_t ld, int m, int n, int row0, int col0,
+                                      int lane, ValueFn&& value, bool out_f16 = false) {
+  typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+  const int lr = lane & 15, lg = lane >> 4;
+  const bool odd = lr & 1;
+  auto swap1 = [](float x) {  // the value of lane ^ 1 (DPP quad_perm [1, 0, 3, 2])
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0xB1, 0xF, 0xF, false));
+  };
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+#pragma unroll
+    for (int j = 0; j < JN; ++j) {
+      float v[4];
+      value(i, j, v);
+      // the even lane keeps rows 0, 1 of the four, the odd one rows 2, 3;
+      // each sends its partner the two values it keeps
+      const float r0 = swap1(odd ? v[0] : v[2]), r1 = swap1(odd ? v[1] : v[3]);
+      const uint32_t w0 = pack16_pair<OUT>(odd ? r0 : v[0], odd ? v[2] : r0, out_f16);
+      const uint32_t w1 = pack16_pair<OUT>(odd ? r1 : v[1], odd ? v[3] : r1, out_f16);
+      const int rr = 16 * j + 4 * lg + (odd ? 2 : 0);
+      const int byte = 2 * (16 * i + (lr & ~1));  // the pair's even m', 4-byte aligned
+      const int q = byte >> 4, within = byte & 15;
+      *reinterpret_cast<uint32_t*>(stg + rr * 128 + ((q ^ (rr & 7)) << 4) + within) = w0;
+      *reinterpret_cast<uint32_t*>(stg + (rr + 1) * 128 + ((q ^ ((rr + 1) & 7)) << 4) + within) = w1;
+    }
+  }
+  // LDS operations of one wave complete in order; the wait keeps the
+  // compiler from moving the reads above the writes.
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+  for (int it = 0; it < 2 * JN; ++it) {
+    const int rr = 8 * it + (lane >> 3);
+    const int q = lane & 7;
+    const u32x4 v = *reinterpret_cast<const u32x4*>(stg + rr * 128 + ((q ^ (rr & 7)) << 4));
+    const int nn = col0 + rr;
+    const int mm = row0 + 8 * q;
+    if (nn < n && mm < m) __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(c + int64_t(nn) * ld + mm));
+  }
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+}
+
 }  // namespace pcamd

@@ -41,6 +41,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <cstdlib>
 #include <cstdint>
 #include <type_traits>
 
@@ -219,9 +220,16 @@ __device__ __attribute__((noinline)) void epilogue_general(void* c, int64_t c_ro
 //     step's first B fragment; the next step's A fragment i is read right
 //     after MFMA (i, 7) has consumed the current one. The last sub-tile's
 //     MFMAs cover the latency of those reads.
-template <bool A_K, bool B_K, int FA, int FB, int MODE, int SBK, int JN, bool KT>
+// JN: 16-column sub-tiles per wave - 8 (256 x 256 tiles), 4 (half tiles of
+// a short last wave) or 7 (256 x 224 tiles). CT: C receives the transpose of
+// this product (the launcher computes C^T = B^T A^T when 224-column tiles
+// fill the waves better); only plain 16-bit outputs take it.
+template <bool A_K, bool B_K, int FA, int FB, int MODE, int SBK, int JN, bool KT, bool CT = false>
 __global__ __launch_bounds__(NT, 1) void bmm_wide_kernel(FastArgs a) {
-  static_assert(JN == 8 || JN == 4, "sub-tiles per wave: 8 (whole tiles) or 4 (half tiles)");
+  static_assert(JN == 8 || JN == 7 || JN == 4, "sub-tiles per wave: 8 (whole tiles), 7 (224-column tiles) or "
+                "4 (half tiles)");
+  static_assert(!CT || JN == 7, "the transposed output goes with 224-column tiles");
+  constexpr int TN = JN == 7 ? 224 : BN;  // tile columns
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   float* sa_tile = reinterpret_cast<float*>(smem + 2 * STAGE);  // [2][BM]
   float* sb_tile = sa_tile + 2 * BM;                             // [2][BN]
@@ -236,8 +244,8 @@ __global__ __launch_bounds__(NT, 1) void bmm_wide_kernel(FastArgs a) {
   // workgroups b and b + 8, on the same XCD, so both read its operands
   // through one L2.
   int pid = blockIdx.x;
-  int wcol = wn * 128;
-  if constexpr (JN == 8) {
+  int wcol = wn * 16 * (JN == 4 ? 8 : JN);
+  if constexpr (JN != 4) {
     if ((a.total_tiles & 7) == 0) pid = (pid & 7) * (a.total_tiles >> 3) + (pid >> 3);
   } else {
     int hsel;
@@ -261,7 +269,7 @@ __global__ __launch_bounds__(NT, 1) void bmm_wide_kernel(FastArgs a) {
   const int gm = min(a.tiles_m - first_m, GROUP_M);
   const int in_group = tile - group * per_group;
   const int m0 = __builtin_amdgcn_readfirstlane((first_m + in_group % gm) * BM);
-  const int n0 = __builtin_amdgcn_readfirstlane((in_group / gm) * BN);
+  const int n0 = __builtin_amdgcn_readfirstlane((in_group / gm) * TN);
 
   const v4i rsa = make_rsrc(a.a + bidx * a.sab, a.a_extent);
   const v4i rsb = make_rsrc(a.b + bidx * a.sbb, a.b_extent);
@@ -397,10 +405,12 @@ __global__ __launch_bounds__(NT, 1) void bmm_wide_kernel(FastArgs a) {
       for (int i = 0; i < 4; ++i) f[i] = sa[i] * sb;
     }
   };
-  auto read_cols = [&](int ks, int j) {
+  // column scales of sub-tile j of step ks into slot `slot` (default j & 1)
+  auto read_cols = [&](int ks, int j, int slot = -1) {
     const float* sbt = sb_tile + (ks & 1) * BN + sb_off + 16 * j;
-    if constexpr (SBK == 1) cs[j & 1].x = sbt[0];
-    if constexpr (SBK == 2) cs[j & 1] = *reinterpret_cast<const float4*>(sbt);
+    const int sl = slot < 0 ? (j & 1) : slot;
+    if constexpr (SBK == 1) cs[sl].x = sbt[0];
+    if constexpr (SBK == 2) cs[sl] = *reinterpret_cast<const float4*>(sbt);
   };
   if constexpr (MODE == 0) {
     read_rows(0, sa_c, fc);
@@ -480,8 +490,13 @@ __global__ __launch_bounds__(NT, 1) void bmm_wide_kernel(FastArgs a) {
   // issued together at the boundary: the same loads in one burst right
   // after the barrier made the forward GEMM of config 5 17 % slower.
   constexpr int kSchedA[4] = {0, 0, 1, 1};
-  constexpr int kSchedB[4] = {JN == 8 ? 2 : 1, JN == 8 ? 2 : 1, JN == 8 ? 3 : 2, JN == 8 ? 3 : 2};
+  constexpr int kSchedB[4] = {JN != 4 ? 2 : 1, JN != 4 ? 2 : 1, JN != 4 ? 3 : 2, JN != 4 ? 3 : 2};
   constexpr int kBReads = B_K ? 2 : 4;  // ds_read instructions per B fragment
+  // The B fragment and column scales of sub-tile j sit in slot j & 1. The
+  // last sub-tile's slot is LAST; at the step boundary the next step's
+  // sub-tile 0 goes to the other slot, and with an odd number of sub-tiles
+  // (JN = 7) it is moved to slot 0 after the last sub-tile.
+  constexpr int LAST = (JN - 1) & 1, FREE = LAST ^ 1;
   auto step = [&](int ks, auto boundary, auto dma, auto scales) {
     constexpr bool BOUNDARY = decltype(boundary)::value;
     constexpr bool DMA = decltype(dma)::value;
@@ -513,23 +528,27 @@ __global__ __launch_bounds__(NT, 1) void bmm_wide_kernel(FastArgs a) {
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
       __syncthreads();
       if constexpr (MODE == 0 && SCALES) sc_next = load_scale(ks + 2);
-      bf[0] = bfrag(nxt, 0);
+      bf[FREE] = bfrag(nxt, 0);
       if constexpr (MODE == 0) {
-        // cs[1] (sub-tile 7) is still needed; cs[0] takes sub-tile 0 of the next step
-        if constexpr (SBK != 0) read_cols(ks + 1, 0);
+        // cs[LAST] (the last sub-tile) is still needed; cs[FREE] takes sub-tile 0 of the next step
+        if constexpr (SBK != 0) read_cols(ks + 1, 0, FREE);
         float sa_n[4], fc_n[4];
         read_rows(ks + 1, sa_n, fc_n);
-        subtile(JN - 1, bf[1], nxt, IC<kBReads + (SBK != 0 ? 1 : 0) + (SBK == 0 ? 3 : 2)>{}, T{});
+        subtile(JN - 1, bf[LAST], nxt, IC<kBReads + (SBK != 0 ? 1 : 0) + (SBK == 0 ? 3 : 2)>{}, T{});
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           sa_c[i] = sa_n[i];
           fc[i] = fc_n[i];
         }
       } else {
-        subtile(JN - 1, bf[1], nxt, IC<kBReads>{}, T{});
+        subtile(JN - 1, bf[LAST], nxt, IC<kBReads>{}, T{});
+      }
+      if constexpr (FREE != 0) {
+        bf[0] = bf[FREE];
+        if constexpr (MODE == 0 && SBK != 0) cs[0] = cs[FREE];
       }
     } else {
-      v8i bcur = bf[1];
+      v8i bcur = bf[LAST];
       if constexpr (MASK) mask_k(bcur);
       subtile(JN - 1, bcur, nullptr, IC<0>{}, F{});
     }
@@ -587,7 +606,8 @@ __global__ __launch_bounds__(NT, 1) void bmm_wide_kernel(FastArgs a) {
                         (a.sbiasm & 3) == 0 && (a.sbiasb & 3) == 0 && (reinterpret_cast<uintptr_t>(a.bias) & 7) == 0;
     const bool out16 = (a.c_dtype == kBF16 || a.c_dtype == kF16) && a.act == PCAMD_ACT_NONE &&
                        (a.bias == nullptr || bias16);
-    if (staged_output_ok(a.c, a.scb, a.scm, a.n, out16)) {
+    // (CT: the launcher checked the transposed output's alignment)
+    if (CT || staged_output_ok(a.c, a.scb, a.scm, a.n, out16)) {
       // each wave stages its sub-tile in 8 KiB (4 KiB for a half tile) of the
       // LDS stage the last K step did not read (no other wave touches it, so no
       // barrier is needed)
@@ -602,38 +622,54 @@ __global__ __launch_bounds__(NT, 1) void bmm_wide_kernel(FastArgs a) {
           store_half_staged<OUT>(smem + (ksteps & 1) * STAGE + wave * 4096, cb, a.scm, a.m, a.n, m0 + wm * 64,
                                  n0 + wcol, lane, value, a.c_dtype == kF16);
       };
-      if (plain) {
-        stage(IC<kBF16>{}, [&](int i, int j, float (&v)[4]) {
+      if constexpr (CT) {
+        // every wave's 14 KiB of staging spans both LDS stages: wait until all
+        // waves have finished reading the last one
+        __syncthreads();
+        auto value = [&](int i, int j, float (&v)[4]) {
           float sbv[4];
           col_scales(j, sbv);
 #pragma unroll
           for (int r = 0; r < 4; ++r) v[r] = out_value(i, j, r, sam_v[i], sbv);
-        });
+        };
+        // C^T's rows are C's columns: its row pitch is C's n stride
+        store_subtile_staged_t<OUT16_RUNTIME, JN>(smem + wave * 16384, cb, a.scn, a.m, a.n, m0 + wm * 64,
+                                                 n0 + wcol, lane, value, a.c_dtype == kF16);
+        return;
+      } else {
+        if (plain) {
+          stage(IC<kBF16>{}, [&](int i, int j, float (&v)[4]) {
+            float sbv[4];
+            col_scales(j, sbv);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) v[r] = out_value(i, j, r, sam_v[i], sbv);
+          });
+          return;
+        }
+        // fp16 output and / or a 16-bit bias, in the reference's order: scaled
+        // product, + bias, one rounding (kernels/bmm/per_block.py:113-137). The
+        // output type is picked per element pair at run time (OUT16_RUNTIME),
+        // so this path is instantiated once.
+        const bool bias_bf16 = a.bias_dtype == kBF16;
+        const uint16_t* bias_b = bias16 ? static_cast<const uint16_t*>(a.bias) + bidx * a.sbiasb : nullptr;
+        auto value = [&](int i, int j, float (&v)[4]) {
+          float sbv[4];
+          col_scales(j, sbv);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) v[r] = out_value(i, j, r, sam_v[i], sbv);
+          const int mm = row_base + 16 * i, nn = col_base + 16 * j;
+          if (bias_b && mm < a.m && nn < a.n) {
+            const uint2 h = *reinterpret_cast<const uint2*>(bias_b + int64_t(mm) * a.sbiasm + nn);
+            const uint32_t e[4] = {h.x & 0xFFFFu, h.x >> 16, h.y & 0xFFFFu, h.y >> 16};
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+              v[r] += bias_bf16 ? __uint_as_float(e[r] << 16)
+                                : static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(e[r])));
+          }
+        };
+        stage(IC<OUT16_RUNTIME>{}, value);
         return;
       }
-      // fp16 output and / or a 16-bit bias, in the reference's order: scaled
-      // product, + bias, one rounding (kernels/bmm/per_block.py:113-137). The
-      // output type is picked per element pair at run time (OUT16_RUNTIME),
-      // so this path is instantiated once.
-      const bool bias_bf16 = a.bias_dtype == kBF16;
-      const uint16_t* bias_b = bias16 ? static_cast<const uint16_t*>(a.bias) + bidx * a.sbiasb : nullptr;
-      auto value = [&](int i, int j, float (&v)[4]) {
-        float sbv[4];
-        col_scales(j, sbv);
-#pragma unroll
-        for (int r = 0; r < 4; ++r) v[r] = out_value(i, j, r, sam_v[i], sbv);
-        const int mm = row_base + 16 * i, nn = col_base + 16 * j;
-        if (bias_b && mm < a.m && nn < a.n) {
-          const uint2 h = *reinterpret_cast<const uint2*>(bias_b + int64_t(mm) * a.sbiasm + nn);
-          const uint32_t e[4] = {h.x & 0xFFFFu, h.x >> 16, h.y & 0xFFFFu, h.y >> 16};
-#pragma unroll
-          for (int r = 0; r < 4; ++r)
-            v[r] += bias_bf16 ? __uint_as_float(e[r] << 16)
-                              : static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(e[r])));
-        }
-      };
-      stage(IC<OUT16_RUNTIME>{}, value);
-      return;
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -669,9 +705,18 @@ __global__ __launch_bounds__(NT, 1) void bmm_wide_kernel(FastArgs a) {
 
 constexpr int LDS_BYTES = 2 * STAGE + 2 * (BM + BN) * 4;
 
-template <bool A_K, bool B_K, int FA, int FB, int MODE, int SBK, int JN, bool KT>
+// PCAMD_BMM_T224=0 keeps the 256 x 256 tiling everywhere (read once)
+inline bool transposed_disabled() {
+  static const bool off = [] {
+    const char* e = getenv("PCAMD_BMM_T224");
+    return e && e[0] == '0';
+  }();
+  return off;
+}
+
+template <bool A_K, bool B_K, int FA, int FB, int MODE, int SBK, int JN, bool KT, bool CT = false>
 int launch_tiles(const FastArgs& a, int grid, hipStream_t st) {
-  auto kern = bmm_wide_kernel<A_K, B_K, FA, FB, MODE, SBK, JN, KT>;
+  auto kern = bmm_wide_kernel<A_K, B_K, FA, FB, MODE, SBK, JN, KT, CT>;
   static std::atomic<uint64_t> configured{0};  // devices whose LDS limit is set
   const int rc = ensure_dynamic_lds(reinterpret_cast<const void*>(kern), LDS_BYTES, st, configured);
   if (rc != 0) return rc;
@@ -696,10 +741,64 @@ int launch_one(const FastArgs& a, hipStream_t st) {
   return launch_tiles<A_K, B_K, FA, FB, MODE, SBK, 4, KT>(half, 2 * tail, st);
 }
 
+// Tile-count model: 256 x 256 tiles take floor(T / CUs) whole waves and a
+// short last wave as half tiles (each about 0.85 of a whole tile) when it
+// fills at most half the CUs. The transposed product C^T = B^T A^T on
+// 256 x 224 tiles takes ceil(T' / CUs) waves of 224 / 256 of a tile each; it
+// is chosen when that is at least 5 % cheaper, e.g. wgrad of config 5
+// (14336 x 4096: 896 tiles = 3.85 tile-times, against 1024 = 4 waves of 224-
+// column tiles, 3.5).
+inline bool transposed_pays(const FastArgs& a, int cus) {
+  if (cus <= 0 || a.total_tiles <= cus) return false;
+  const int tail = a.total_tiles % cus;
+  const double now = a.total_tiles / cus + (tail == 0 ? 0.0 : 2 * tail <= cus ? 0.85 : 1.0);
+  const int64_t batch = a.total_tiles / a.tiles_per_batch;
+  const int64_t t2 = int64_t((a.n + BM - 1) / BM) * ((a.m + 223) / 224) * batch;
+  const double alt = double((t2 + cus - 1) / cus) * (224.0 / 256.0);
+  return alt < 0.95 * now;
+}
+
+// The transposed launch's arguments: A' = B^T, B' = A^T, C' = C^T (rows of
+// C' are C's columns), block scales with their roles swapped. Plain 16-bit C
+// only (its staged store writes C's rows of 16-byte chunks), and every offset
+// the 224-column tiles form (they load 256 columns) inside 32 bits.
+inline bool transposed_args(const FastArgs& a, bool a_k, FastArgs& t) {
+  if (a.bias != nullptr || a.act != PCAMD_ACT_NONE || (a.c_dtype != kBF16 && a.c_dtype != kF16)) return false;
+  if (a.scn != 1 || (a.scm & 7) || (a.scb & 7) || (a.n & 7) || (reinterpret_cast<uintptr_t>(a.c) & 15))
+    return false;
+  const int64_t kpad = (a.k + BK - 1) / BK * BK;
+  const int64_t rows = int64_t((a.m + 223) / 224) * 224 + 32;  // A's rows (or columns) the tiles reach
+  const int64_t amax = a_k ? rows * a.lda + kpad : (kpad - 1) * int64_t(a.lda) + rows;
+  if (amax >= (int64_t{1} << 32) - 64) return false;
+  t = a;
+  t.a = a.b; t.b = a.a;
+  t.sab = a.sbb; t.sbb = a.sab;
+  t.lda = a.ldb; t.ldb = a.lda;
+  t.a_extent = a.b_extent; t.b_extent = a.a_extent;
+  t.m = a.n; t.n = a.m;
+  t.scm = a.scn; t.scn = a.scm;
+  t.sa = a.sb; t.sb = a.sa;
+  t.ssab = a.ssbb; t.ssa1 = a.ssb2; t.ssa2 = a.ssb1;  // A' = B^T: rows are B's columns
+  t.ssbb = a.ssab; t.ssb1 = a.ssa2; t.ssb2 = a.ssa1;  // B' = A^T: columns are A's rows
+  t.qbm_shift = a.qbn_shift; t.qbn_shift = a.qbm_shift;
+  t.tiles_m = (t.m + BM - 1) / BM;
+  t.tiles_n = (t.n + 223) / 224;
+  t.tiles_per_batch = t.tiles_m * t.tiles_n;
+  t.total_tiles = t.tiles_per_batch * (a.total_tiles / a.tiles_per_batch);
+  t.tile_base = 0;
+  return true;
+}
+
 // block mode: B-scale kind from the quant block width (qbn = 1 << qbn_shift):
 // >= 128 one scale per wave, >= 16 one per 16-column sub-tile, else per column
 template <bool A_K, bool B_K, int FA, int FB, bool KT>
 int launch_mode(const FastArgs& a, int mode, hipStream_t st) {
+  // A with one scale per row (qbm = 1): the transposed kernel's B' has one
+  // scale per column, the wgrad recipe's 128 x 1 x 128 x 1 product
+  FastArgs t;
+  if (mode == 0 && a.qbm_shift == 0 && transposed_pays(a, device_cu_count(st)) && transposed_args(a, A_K, t) &&
+      !transposed_disabled())
+    return launch_tiles<B_K, A_K, FB, FA, 0, 2, 7, KT, true>(t, t.total_tiles, st);
   if (mode == 1) return launch_one<A_K, B_K, FA, FB, 1, 0, KT>(a, st);
   if (mode == 2) return launch_one<A_K, B_K, FA, FB, 2, 0, KT>(a, st);
   if (a.qbn_shift >= 7) return launch_one<A_K, B_K, FA, FB, 0, 0, KT>(a, st);
