@@ -39,10 +39,13 @@ SETTLE_MS = 100.0            # untimed load before the first (headline) measurem
 # the kernels configs 4 and 5 launch (as rocprofv3 names them), to match the
 # committed counter summary (profiles/pmc_bmm.json) to the code that runs now
 CONFIG4_KERNEL = "pcamd::bmms::bmm_stream_kernel<3>"
-CONFIG5_KERNELS = {"fwd_a_k_b_k": ("fwd", ["pcamd::bmmw::bmm_wide_kernel<true, true, 3, 0, 0, 8>"]),
-                   "dgrad_a_k_b_n": ("dgrad", ["pcamd::bmmw::bmm_wide_kernel<true, false, 3, 0, 0, 8>"]),
-                   "wgrad_a_m_b_n": ("wgrad_a_m_b_n", ["pcamd::bmmw::bmm_wide_kernel<false, false, 3, 0, 2, 4>",
-                                                       "pcamd::bmmw::bmm_wide_kernel<false, false, 3, 0, 2, 8>"])}
+# template arguments: A K-major, B K-major, A / B fp8 formats, scale mode, B-scale kind,
+# sub-tiles per wave, ragged K, transposed output (wgrad: 256 x 224 tiles of C^T)
+CONFIG5_KERNELS = {"fwd_a_k_b_k": ("fwd", ["pcamd::bmmw::bmm_wide_kernel<true, true, 3, 3, 0, 0, 8, false, false>"]),
+                   "dgrad_a_k_b_n": ("dgrad",
+                                     ["pcamd::bmmw::bmm_wide_kernel<true, false, 3, 3, 0, 0, 8, false, false>"]),
+                   "wgrad_a_m_b_n": ("wgrad_a_m_b_n",
+                                     ["pcamd::bmmw::bmm_wide_kernel<false, false, 3, 3, 0, 2, 7, false, true>"])}
 
 
 def pmc_field(workload, kernels, keys):
@@ -86,6 +89,9 @@ def parse():
                    help="the reference's 31 published per-tensor fp8 BMM shapes (fp16 C + fp16 bias, "
                         "B N-major / K-major as published): 'graph' times them (one JSON line), 'eager' "
                         "launches each 3 times for rocprofv3")
+    p.add_argument("--fused", action="store_true",
+                   help="the fused activation-quant BMM (pcamd_bmm_quant_a) against quantize-then-multiply, "
+                        "bf16 A [M, 4096] x e4m3 B [4096, N] 128x128-scaled, over N (one JSON line)")
     p.add_argument("--repack", action="store_true",
                    help="the transpose variants' operand copy at the config-5 shapes: torch's strided "
                         "copy (the reference's .contiguous()) next to pcamd_repack_fp8 (one JSON line)")
@@ -944,6 +950,38 @@ def published_bmm(torch, dev, steps, warmup, eager):
                           "unstated hardware (context, not a target)"}))
 
 
+def fused_probe(torch, dev, steps, warmup):
+    """pcamd_bmm_quant_a (A quantized 1x128 inside the GEMM's K loop) next to
+    its unfused equal (hip_per_block_quant, then hip_per_block_bmm), graph-
+    timed on the same inputs: bf16 A [M, K], e4m3 B [K, N] (N-major,
+    128x128 scales), bf16 C. The fused kernel quantizes each A row block once
+    per N tile, so it wins where few N tiles share A (small N) and loses as N
+    grows."""
+    from practice_cuda_amd.impls.hip_per_block import (hip_per_block_bmm, hip_per_block_bmm_quant_a,
+                                                       hip_per_block_quant)
+    g = torch.Generator(device=dev).manual_seed(0)
+    rows = []
+    for m, k, n in [(32768, 4096, 128), (32768, 4096, 256), (16384, 4096, 512), (8192, 4096, 1024),
+                    (8192, 4096, 4096), (8192, 4096, 14336)]:
+        x = torch.randn(1, m, k, generator=g, device=dev).bfloat16()
+        qb = hip_per_block_quant((torch.randn(1, k, n, generator=g, device=dev) * 0.02).bfloat16(),
+                                 block_m=128, block_n=128)
+        out = torch.empty(1, m, n, device=dev, dtype=torch.bfloat16)
+        fused_ms, _ = graph_time(torch, lambda i: hip_per_block_bmm_quant_a(x, qb, out=out), steps, warmup)
+
+        def unfused(i):
+            hip_per_block_bmm(hip_per_block_quant(x, block_m=1, block_n=128), qb, out=out)
+
+        unfused_ms, _ = graph_time(torch, unfused, steps, warmup)
+        rows.append({"m": m, "k": k, "n": n, "fused_us": round(fused_ms * 1e3, 1),
+                     "quantize_then_multiply_us": round(unfused_ms * 1e3, 1),
+                     "fused_speedup": round(unfused_ms / fused_ms, 3)})
+        print(rows[-1], file=sys.stderr, flush=True)
+        del x, qb, out
+        torch.cuda.empty_cache()
+    print(json.dumps({"fused_quant_bmm": rows}))
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -971,6 +1009,9 @@ def main():
         return
     if args.repack:
         repack_probe(torch, dev, args.steps, args.warmup)
+        return
+    if args.fused:
+        fused_probe(torch, dev, args.steps, args.warmup)
         return
     if args.published:
         published_bmm(torch, dev, args.steps, args.warmup, args.published == "eager")
