@@ -45,6 +45,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <cstddef>
 #include <cstdint>
 #include <cstdlib>
 
@@ -57,23 +58,30 @@ constexpr int kThreads = 256;
 constexpr int kMaxSlots = 16;  // chunk slots held in registers per lane
 
 // ===========================================================================
-// row-contiguous kernels (persistent waves, next unit prefetched in registers)
+// row-contiguous kernels: one wave or one workgroup per unit
 // ===========================================================================
+// Field order: everything the flat group kernel reads sits in the first 48
+// bytes, one 64-byte line of the kernel-argument segment. Its waves test
+// `units` before loading anything else, so with the fields spread over two
+// lines the first wave on a CU waited for two scalar-cache misses in a row:
+// config 1 15.90-15.97 us against 15.56-15.65 us packed (16 rotating buffer
+// sets, same kernel code).
 struct RowArgs {
   const char* x;
   uint8_t* y;
   float* scale;
+  int64_t total;    // chunks of the whole tensor (flat group kernel)
+  uint32_t units;   // rows * segs
+  int32_t chunks;   // 8-element chunks per row
+  float fp8_max, eps;
   uint32_t m;       // rows per batch
+  uint32_t segs;    // segments per row (group kernel)
+  int32_t cpl;      // chunk slots per lane (wave-per-row kernel)
   int64_t sxb, sxm; // input strides (elements)
   int64_t syb, sym; // output strides (bytes == elements)
   int64_t ssb, ssm, ssn;  // scale strides (elements)
-  uint32_t units;   // rows * segs
-  int32_t chunks;   // 8-element chunks per row
-  int32_t cpl;      // chunk slots per lane (wave-per-row kernel)
-  uint32_t segs;    // segments per row (group kernel)
-  int64_t total;    // chunks of the whole tensor (flat group kernel)
-  float fp8_max, eps;
 };
+static_assert(offsetof(RowArgs, eps) + sizeof(float) <= 64, "flat group kernel fields in one 64-byte line");
 
 typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
 
@@ -92,7 +100,12 @@ PCAMD_DEV void store8(uint8_t* p, uint2 v) {
 // workgroup). FLAT: input, output and scales are contiguous and the row
 // length is a multiple of the group, so the tensor is one run of chunks
 // (units may span rows, groups never do) and no row index is needed.
-constexpr int kGroupThreads = 128;
+// 256-thread workgroups: config 1 ([4096, 7168] bf16, 16 rotating buffer
+// sets) 16.04-16.14 -> 15.57-15.67 us against 128 threads; 64 and 512
+// threads sat in between.
+constexpr int kGroupThreads = 256;
+// the per-tensor quantize pass keeps its measured 128-thread workgroups
+constexpr int kTensorFlatThreads = 128;
 
 template <int DT, int FMT, int LPG, int CPL, bool NTS, bool FLAT, bool CLAMP>
 __global__ __launch_bounds__(kGroupThreads) void quant_groups_kernel(RowArgs a) {
@@ -239,6 +252,7 @@ struct TileArgs {
   int32_t block_m;
   int32_t cpt;       // chunks per thread = block_m * lpr / 256
   int32_t lpr, lpr_shift;  // lanes per block row (block_n / 8) and its log2
+  int32_t four;      // 1: 128 x 128 blocks, four per workgroup (quant_tile4_kernel)
   float fp8_max, eps;
 };
 
@@ -294,6 +308,48 @@ __global__ __launch_bounds__(kThreads) void quant_tile_kernel(TileArgs a) {
       block(b, pm, rem - pm * a.nb, red[it & 1]);  // alternating slots: one barrier per block
     }
   }
+}
+
+// Four 128 x 128 blocks side by side per workgroup (128 rows x 512 columns,
+// 1024 threads) for 16-bit row-contiguous input with m a multiple of 128 and
+// n of 512: wave w owns rows w, w + 16, ..., so one load instruction of a
+// wave reads 1 KiB of one row (64 lanes x 16 bytes, lanes 16 q .. 16 q + 15
+// in block q) and one store writes 512 contiguous bytes. The lanes of a
+// block reduce in their 16-lane row by DPP, the 16 waves through LDS. Grid
+// (n / 512, m / 128, batch). Config 3 ([4096, 7168] bf16, 16 rotating buffer
+// sets): 16.47-16.65 -> 15.94-16.18 us against one block per 256-thread
+// workgroup (4 rows x 256 bytes per load instruction).
+constexpr int kTile4Threads = 1024;
+
+template <int DT, int FMT, bool NTS, bool CLAMP>
+__global__ __launch_bounds__(kTile4Threads) void quant_tile4_kernel(TileArgs a) {
+  static_assert(DT == kBF16 || DT == kF16, "16-bit inputs: one 16-byte load per chunk");
+  constexpr int EB = elem_bytes<DT>();
+  constexpr int WAVES = kTile4Threads / 64, ROWS = 128 / WAVES;  // 8 chunks per thread
+  __shared__ uint32_t red[WAVES][4];
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6, q = lane >> 4;
+  const int64_t r0 = int64_t(blockIdx.y) * 128 + wave;
+  const int64_t col = int64_t(blockIdx.x) * 512 + lane * 8;
+  const char* xb = a.x + (int64_t(blockIdx.z) * a.sxb + col) * EB;
+  Chunk<DT> cur[ROWS];
+#pragma unroll
+  for (int p = 0; p < ROWS; ++p) load_chunk<DT>(cur[p], xb + (r0 + p * WAVES) * a.sxm * EB);
+  float amax = 0.0f;
+#pragma unroll
+  for (int p = 0; p < ROWS; ++p) amax = fmaxf(amax, chunk_amax<DT>(cur[p]));
+  const uint32_t u = __float_as_uint(group_max<16>(amax));
+  if ((lane & 15) == 0) red[wave][q] = u;
+  __syncthreads();
+  uint32_t mx = red[0][q];
+#pragma unroll
+  for (int w = 1; w < WAVES; ++w) mx = max(mx, red[w][q]);  // non-negative floats order like their bits
+  const Scales s = block_scales(__uint_as_float(mx), a.fp8_max, a.eps);
+  if (wave == 0 && (lane & 15) == 0)
+    a.scale[int64_t(blockIdx.z) * a.ssb + int64_t(blockIdx.y) * a.ssm + int64_t(blockIdx.x * 4 + q) * a.ssn] = s.ds;
+  uint8_t* yb = a.y + int64_t(blockIdx.z) * a.syb + col;
+#pragma unroll
+  for (int p = 0; p < ROWS; ++p)
+    store8<DT, NTS>(yb + (r0 + p * WAVES) * a.sym, quant_chunk<DT, FMT, CLAMP>(cur[p], s.qs, a.fp8_max));
 }
 
 // ===========================================================================
@@ -580,11 +636,11 @@ __global__ __launch_bounds__(kAmaxThreads) void tensor_amax_flat_kernel(TensorAr
 }
 
 template <int DT, int FMT, bool NTS>
-__global__ __launch_bounds__(kGroupThreads) void tensor_quant_flat_kernel(TensorArgs a) {
+__global__ __launch_bounds__(kTensorFlatThreads) void tensor_quant_flat_kernel(TensorArgs a) {
   constexpr int EB = elem_bytes<DT>(), CPL = 2;
   const int64_t chunks = a.total / 8;
   const int lane = threadIdx.x & 63;
-  const int64_t u = int64_t(blockIdx.x) * (kGroupThreads / 64) + (threadIdx.x >> 6);
+  const int64_t u = int64_t(blockIdx.x) * (kTensorFlatThreads / 64) + (threadIdx.x >> 6);
   const int64_t ch0 = u * (CPL * 64) + lane;
   Chunk<DT> cur[CPL];
 #pragma unroll
@@ -1170,6 +1226,23 @@ struct LaunchTile {
   static int go(const TileArgs& a, hipStream_t st) {
     return clamp_free<FMT>(a.fp8_max, a.eps) ? go2<CPT, NTS, false>(a, st) : go2<CPT, NTS, true>(a, st);
   }
+  // 128 x 128 blocks of 16-bit input, four per workgroup (m % 128 == 0,
+  // n % 512 == 0; the host checked the grid limits)
+  template <bool NTS, bool CLAMP>
+  static int four(const TileArgs& a, hipStream_t st) {
+    const dim3 grid(static_cast<uint32_t>(a.n / 512), a.mb, a.blocks / (a.mb * a.nb));
+    quant_tile4_kernel<DT, FMT, NTS, CLAMP><<<grid, kTile4Threads, 0, st>>>(a);
+    return check_launch("quant_tile4_kernel");
+  }
+  static int run_four(const TileArgs& a, hipStream_t st) {
+    if constexpr (DT == kF32) {
+      return set_error(PCAMD_ERR_UNSUPPORTED, "four-block tile kernel: 16-bit inputs only");
+    } else {
+      const bool cf = clamp_free<FMT>(a.fp8_max, a.eps);
+      if (nt_stores()) return cf ? four<true, false>(a, st) : four<true, true>(a, st);
+      return cf ? four<false, false>(a, st) : four<false, true>(a, st);
+    }
+  }
   template <int CPT, bool NTS, bool CLAMP>
   static int go2(const TileArgs& a, hipStream_t st) {
     const uint32_t batch = a.blocks / (a.mb * a.nb);
@@ -1194,7 +1267,10 @@ struct LaunchTile {
       default: return set_error(PCAMD_ERR_UNSUPPORTED, "tile kernel: unsupported chunks per thread %d", a.cpt);
     }
   }
-  static int run(const TileArgs& a, hipStream_t st) { return nt_stores() ? by_cpt<true>(a, st) : by_cpt<false>(a, st); }
+  static int run(const TileArgs& a, hipStream_t st) {
+    if (a.four) return run_four(a, st);
+    return nt_stores() ? by_cpt<true>(a, st) : by_cpt<false>(a, st);
+  }
 };
 
 template <int DT, int FMT>
@@ -1294,9 +1370,9 @@ struct LaunchTensor {
       const int64_t chunks = a.total / 8;
       tensor_amax_flat_kernel<DT><<<grid_for(chunks, kAmaxThreads * 8, kAmaxGrid), kAmaxThreads, 0, st>>>(a);
       const int64_t waves = (chunks + 127) / 128;
-      const int grid = static_cast<int>((waves + kGroupThreads / 64 - 1) / (kGroupThreads / 64));
-      if (nt_stores()) tensor_quant_flat_kernel<DT, FMT, true><<<grid, kGroupThreads, 0, st>>>(a);
-      else tensor_quant_flat_kernel<DT, FMT, false><<<grid, kGroupThreads, 0, st>>>(a);
+      const int grid = static_cast<int>((waves + kTensorFlatThreads / 64 - 1) / (kTensorFlatThreads / 64));
+      if (nt_stores()) tensor_quant_flat_kernel<DT, FMT, true><<<grid, kTensorFlatThreads, 0, st>>>(a);
+      else tensor_quant_flat_kernel<DT, FMT, false><<<grid, kTensorFlatThreads, 0, st>>>(a);
     } else if (a.total > 0) {
       const int grid = grid_for(a.total, kThreads, 4096);
       tensor_amax_kernel<DT><<<grid, kThreads, 0, st>>>(a);
@@ -1399,6 +1475,10 @@ extern "C" int pcamd_quant_block(const void* x, int x_dtype, int64_t batch, int6
     a.lpr_shift = 0;
     while ((1 << a.lpr_shift) < a.lpr) ++a.lpr_shift;
     a.fp8_max = fp8_max; a.eps = eps;
+    // 128 x 128 blocks of 16-bit input tiling the tensor in 128 x 512 strips:
+    // four blocks per workgroup
+    a.four = block_m == 128 && block_n == 128 && x_dtype != kF32 && m % 128 == 0 && n % 512 == 0 &&
+             mb <= 65535 && batch <= 65535 && n / 512 <= INT32_MAX;
     return dispatch_dt_fmt<LaunchTile>(x_dtype, y_dtype, a, st);
   }
   if (fast && block_n == 1 && block_m >= 16 && block_m <= 256) {
