@@ -252,7 +252,7 @@ struct TileArgs {
   int32_t block_m;
   int32_t cpt;       // chunks per thread = block_m * lpr / 256
   int32_t lpr, lpr_shift;  // lanes per block row (block_n / 8) and its log2
-  int32_t four;      // 1: 128 x 128 blocks, four per workgroup (quant_tile4_kernel)
+  int32_t wide;      // H > 0: 128 x 128 blocks, 4 H per workgroup (quant_tile_wide_kernel)
   float fp8_max, eps;
 };
 
@@ -310,46 +310,64 @@ __global__ __launch_bounds__(kThreads) void quant_tile_kernel(TileArgs a) {
   }
 }
 
-// Four 128 x 128 blocks side by side per workgroup (128 rows x 512 columns,
-// 1024 threads) for 16-bit row-contiguous input with m a multiple of 128 and
-// n of 512: wave w owns rows w, w + 16, ..., so one load instruction of a
-// wave reads 1 KiB of one row (64 lanes x 16 bytes, lanes 16 q .. 16 q + 15
-// in block q) and one store writes 512 contiguous bytes. The lanes of a
-// block reduce in their 16-lane row by DPP, the 16 waves through LDS. Grid
-// (n / 512, m / 128, batch). Config 3 ([4096, 7168] bf16, 16 rotating buffer
-// sets): 16.47-16.65 -> 15.94-16.18 us against one block per 256-thread
-// workgroup (4 rows x 256 bytes per load instruction).
-constexpr int kTile4Threads = 1024;
+// 128 x 128 blocks of 16-bit row-contiguous input, 4 H side by side per
+// 1024-thread workgroup (128 rows x 512 H columns; m a multiple of 128, n of
+// 512 H). Wave w owns rows w, w + 16, ..., and each lane H chunks of a row
+// 512 columns apart, so one row piece of a wave is H KiB read by H load
+// instructions of 1 KiB (64 lanes x 16 bytes; lanes 16 q .. 16 q + 15 of
+// instruction h in block q + 4 h) and written by H stores of 512 bytes. The
+// lanes of a block reduce in their 16-lane row by DPP, the 16 waves through
+// LDS. Grid (n / (512 H), m / 128, batch). Config 3 ([4096, 7168] bf16, 16
+// rotating buffer sets), against one block per 256-thread workgroup (4 rows x
+// 256 bytes per load instruction) at 15.9-16.1 us: H = 1 (1 KiB row pieces)
+// 15.9-16.1 us, H = 2 (2 KiB) 14.66-14.72 us. The host takes it only for
+// grids of at most one workgroup per CU (pcamd_quant_block).
+constexpr int kTileWideThreads = 1024;
 
-template <int DT, int FMT, bool NTS, bool CLAMP>
-__global__ __launch_bounds__(kTile4Threads) void quant_tile4_kernel(TileArgs a) {
+template <int DT, int FMT, int H, bool NTS, bool CLAMP>
+__global__ __launch_bounds__(kTileWideThreads) void quant_tile_wide_kernel(TileArgs a) {
   static_assert(DT == kBF16 || DT == kF16, "16-bit inputs: one 16-byte load per chunk");
+  static_assert(H == 1 || H == 2, "four or eight blocks per workgroup");
   constexpr int EB = elem_bytes<DT>();
-  constexpr int WAVES = kTile4Threads / 64, ROWS = 128 / WAVES;  // 8 chunks per thread
-  __shared__ uint32_t red[WAVES][4];
+  constexpr int WAVES = kTileWideThreads / 64, ROWS = 128 / WAVES;  // 8 rows x H chunks per thread
+  __shared__ uint32_t red[WAVES][4 * H];
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6, q = lane >> 4;
   const int64_t r0 = int64_t(blockIdx.y) * 128 + wave;
-  const int64_t col = int64_t(blockIdx.x) * 512 + lane * 8;
+  const int64_t col = int64_t(blockIdx.x) * (512 * H) + lane * 8;
   const char* xb = a.x + (int64_t(blockIdx.z) * a.sxb + col) * EB;
-  Chunk<DT> cur[ROWS];
+  Chunk<DT> cur[ROWS][H];
 #pragma unroll
-  for (int p = 0; p < ROWS; ++p) load_chunk<DT>(cur[p], xb + (r0 + p * WAVES) * a.sxm * EB);
-  float amax = 0.0f;
+  for (int p = 0; p < ROWS; ++p)
 #pragma unroll
-  for (int p = 0; p < ROWS; ++p) amax = fmaxf(amax, chunk_amax<DT>(cur[p]));
-  const uint32_t u = __float_as_uint(group_max<16>(amax));
-  if ((lane & 15) == 0) red[wave][q] = u;
+    for (int h = 0; h < H; ++h) load_chunk<DT>(cur[p][h], xb + ((r0 + p * WAVES) * a.sxm + h * 512) * EB);
+  float qs[H];
+#pragma unroll
+  for (int h = 0; h < H; ++h) {
+    float amax = 0.0f;
+#pragma unroll
+    for (int p = 0; p < ROWS; ++p) amax = fmaxf(amax, chunk_amax<DT>(cur[p][h]));
+    const uint32_t u = __float_as_uint(group_max<16>(amax));
+    if ((lane & 15) == 0) red[wave][4 * h + q] = u;
+  }
   __syncthreads();
-  uint32_t mx = red[0][q];
 #pragma unroll
-  for (int w = 1; w < WAVES; ++w) mx = max(mx, red[w][q]);  // non-negative floats order like their bits
-  const Scales s = block_scales(__uint_as_float(mx), a.fp8_max, a.eps);
-  if (wave == 0 && (lane & 15) == 0)
-    a.scale[int64_t(blockIdx.z) * a.ssb + int64_t(blockIdx.y) * a.ssm + int64_t(blockIdx.x * 4 + q) * a.ssn] = s.ds;
+  for (int h = 0; h < H; ++h) {
+    uint32_t mx = red[0][4 * h + q];
+#pragma unroll
+    for (int w = 1; w < WAVES; ++w) mx = max(mx, red[w][4 * h + q]);  // non-negative floats order like their bits
+    const Scales s = block_scales(__uint_as_float(mx), a.fp8_max, a.eps);
+    qs[h] = s.qs;
+    if (wave == 0 && (lane & 15) == 0)
+      a.scale[int64_t(blockIdx.z) * a.ssb + int64_t(blockIdx.y) * a.ssm +
+              int64_t(blockIdx.x * 4 * H + 4 * h + q) * a.ssn] = s.ds;
+  }
   uint8_t* yb = a.y + int64_t(blockIdx.z) * a.syb + col;
 #pragma unroll
   for (int p = 0; p < ROWS; ++p)
-    store8<DT, NTS>(yb + (r0 + p * WAVES) * a.sym, quant_chunk<DT, FMT, CLAMP>(cur[p], s.qs, a.fp8_max));
+#pragma unroll
+    for (int h = 0; h < H; ++h)
+      store8<DT, NTS>(yb + (r0 + p * WAVES) * a.sym + h * 512,
+                      quant_chunk<DT, FMT, CLAMP>(cur[p][h], qs[h], a.fp8_max));
 }
 
 // ===========================================================================
@@ -1226,21 +1244,22 @@ struct LaunchTile {
   static int go(const TileArgs& a, hipStream_t st) {
     return clamp_free<FMT>(a.fp8_max, a.eps) ? go2<CPT, NTS, false>(a, st) : go2<CPT, NTS, true>(a, st);
   }
-  // 128 x 128 blocks of 16-bit input, four per workgroup (m % 128 == 0,
-  // n % 512 == 0; the host checked the grid limits)
-  template <bool NTS, bool CLAMP>
-  static int four(const TileArgs& a, hipStream_t st) {
-    const dim3 grid(static_cast<uint32_t>(a.n / 512), a.mb, a.blocks / (a.mb * a.nb));
-    quant_tile4_kernel<DT, FMT, NTS, CLAMP><<<grid, kTile4Threads, 0, st>>>(a);
-    return check_launch("quant_tile4_kernel");
+  // 128 x 128 blocks of 16-bit input, 4 H per workgroup (m % 128 == 0,
+  // n % (512 H) == 0; the host checked the grid limits)
+  template <int H, bool NTS, bool CLAMP>
+  static int wide(const TileArgs& a, hipStream_t st) {
+    const dim3 grid(static_cast<uint32_t>(a.n / (512 * H)), a.mb, a.blocks / (a.mb * a.nb));
+    quant_tile_wide_kernel<DT, FMT, H, NTS, CLAMP><<<grid, kTileWideThreads, 0, st>>>(a);
+    return check_launch("quant_tile_wide_kernel");
   }
-  static int run_four(const TileArgs& a, hipStream_t st) {
+  template <int H>
+  static int run_wide(const TileArgs& a, hipStream_t st) {
     if constexpr (DT == kF32) {
-      return set_error(PCAMD_ERR_UNSUPPORTED, "four-block tile kernel: 16-bit inputs only");
+      return set_error(PCAMD_ERR_UNSUPPORTED, "wide tile kernel: 16-bit inputs only");
     } else {
       const bool cf = clamp_free<FMT>(a.fp8_max, a.eps);
-      if (nt_stores()) return cf ? four<true, false>(a, st) : four<true, true>(a, st);
-      return cf ? four<false, false>(a, st) : four<false, true>(a, st);
+      if (nt_stores()) return cf ? wide<H, true, false>(a, st) : wide<H, true, true>(a, st);
+      return cf ? wide<H, false, false>(a, st) : wide<H, false, true>(a, st);
     }
   }
   template <int CPT, bool NTS, bool CLAMP>
@@ -1268,7 +1287,8 @@ struct LaunchTile {
     }
   }
   static int run(const TileArgs& a, hipStream_t st) {
-    if (a.four) return run_four(a, st);
+    if (a.wide == 2) return run_wide<2>(a, st);
+    if (a.wide == 1) return run_wide<1>(a, st);
     return nt_stores() ? by_cpt<true>(a, st) : by_cpt<false>(a, st);
   }
 };
@@ -1475,10 +1495,23 @@ extern "C" int pcamd_quant_block(const void* x, int x_dtype, int64_t batch, int6
     a.lpr_shift = 0;
     while ((1 << a.lpr_shift) < a.lpr) ++a.lpr_shift;
     a.fp8_max = fp8_max; a.eps = eps;
-    // 128 x 128 blocks of 16-bit input tiling the tensor in 128 x 512 strips:
-    // four blocks per workgroup
-    a.four = block_m == 128 && block_n == 128 && x_dtype != kF32 && m % 128 == 0 && n % 512 == 0 &&
-             mb <= 65535 && batch <= 65535 && n / 512 <= INT32_MAX;
+    // 128 x 128 blocks of 16-bit input: the 1024-thread kernel with 4 H blocks
+    // per workgroup when its grid puts at most one workgroup on each CU and
+    // fills at least 60 % of them (the whole tensor in flight at once, every
+    // CU streaming one 128-row strip piece). Measured on [4096, n] bf16: H = 2
+    // 8-14 % faster than one block per 256-thread workgroup at n = 5120-7168
+    // (160-224 workgroups), H = 1 9-15 % faster at n = 3072 and 4096 (192 and
+    // 256); with more workgroups than CUs (n >= 9216 for H = 2) both were
+    // 4-23 % slower, and H = 2 with rows of a multiple of 8 KiB ([8192, 4096])
+    // 19 % slower at one workgroup per CU.
+    if (block_m == 128 && block_n == 128 && x_dtype != kF32 && m % 128 == 0 && mb <= 65535 && batch <= 65535 &&
+        n / 512 <= INT32_MAX) {
+      const int64_t cus = device_cu_count(st);
+      auto fits = [&](int64_t wgs) { return cus > 0 && wgs <= cus && 10 * wgs >= 6 * cus; };
+      const int64_t strips = batch * mb;
+      if (n % 1024 == 0 && (sxm * 2) % 8192 != 0 && fits(strips * (n / 1024))) a.wide = 2;
+      else if (n % 512 == 0 && fits(strips * (n / 512))) a.wide = 1;
+    }
     return dispatch_dt_fmt<LaunchTile>(x_dtype, y_dtype, a, st);
   }
   if (fast && block_n == 1 && block_m >= 16 && block_m <= 256) {

@@ -118,8 +118,11 @@ BLOCK_CASES = [
     ((5, 2048), "bf16", 1, 512, "e5m2"),        # rows, 1x512 (whole wave per group)
     ((9, 9000), "bf16", 1, 128, "e4m3"),        # rows, two segments per row
     ((256, 384), "bf16", 128, 128, "e4m3"),     # tile
-    ((256, 512), "bf16", 128, 128, "e4m3"),     # tile, four blocks per workgroup
-    ((2, 128, 1024), "f16", 128, 128, "e5m2"),  # tile, four blocks per workgroup, batch, fp16
+    # the 1024-thread tile kernel is taken for grids of one workgroup per CU
+    # (256 CUs: 154-256 workgroups of 128 rows x 512 H columns)
+    ((4096, 4096), "bf16", 128, 128, "e4m3"),     # tile, four blocks per workgroup (256 workgroups)
+    ((2, 2048, 4096), "bf16", 128, 128, "e4m3"),  # tile, four blocks per workgroup, batch
+    ((2, 2048, 7168), "f16", 128, 128, "e5m2"),   # tile, eight blocks per workgroup, batch, fp16
     ((2, 300, 264), "bf16", 128, 128, "e4m3"),  # tile, ragged blocks
     ((64, 256), "bf16", 64, 64, "e5m2"),        # tile, 64x64
     ((128, 512), "f32", 128, 256, "e4m3"),      # tile, 128x256, fp32
@@ -158,15 +161,15 @@ def test_block_quant_strided_input(dev):
     assert_same(r, q_ref, s_ref, "transposed")
 
 
-def test_four_block_tiles_padded_rows(dev):
-    # the four-block 128 x 128 kernel on rows of a wider 3-D tensor (row pitch
-    # 1152 elements in, 1024 out): input and output strides differ
-    base = make_input((2, 256, 1152), "bf16", seed=12, scale=0.5, outliers=0.002).to(dev)
-    x = base[:, :, :1024]
-    print("four-block tiles, row pitch 1152", flush=True)
+def test_wide_tiles_padded_rows(dev):
+    # the eight-block 128 x 128 kernel on rows of a wider 3-D tensor (row pitch
+    # 7296 elements in, 7168 out): input and output strides differ
+    base = make_input((2, 2048, 7296), "bf16", seed=12, scale=0.5, outliers=0.002).to(dev)
+    x = base[:, :, :7168]
+    print("eight-block tiles, row pitch 7296", flush=True)
     r = hip_per_block_quant(x, block_m=128, block_n=128)
     q_ref, s_ref = O.quant_block(x.cpu().contiguous(), 128, 128)
-    assert_same(r, q_ref, s_ref, "four-block tiles, padded rows")
+    assert_same(r, q_ref, s_ref, "eight-block tiles, padded rows")
 
 
 @pytest.mark.parametrize("bm,bn", [(1, 128), (1, 64), (128, 128), (128, 1), (32, 1)])
@@ -578,7 +581,7 @@ REDUCED_PATHS = [
     ("block", (64, 1024), "bf16", 1, 128),        # row groups, flat
     ("block", (3, 40, 1000), "f32", 1, 128),      # row groups, ragged
     ("block", (256, 384), "bf16", 128, 128),      # tiles, whole
-    ("block", (128, 1024), "bf16", 128, 128),     # tiles, four blocks per workgroup
+    ("block", (4096, 5120), "bf16", 128, 128),    # tiles, eight blocks per workgroup (160)
     ("block", (200, 300), "f16", 128, 128),       # tiles, partial
     ("block", (300, 256), "bf16", 128, 1),        # column groups
     ("block", (50, 70), "f16", 4, 16),            # generic
