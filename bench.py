@@ -324,6 +324,7 @@ def bench_config4(torch, steps, warmup, dev, nsets=4):
 
 
 CONFIG5_DIMS = (8192, 4096, 14336)  # M (tokens), K (in features), N (out features)
+CONFIG5_SETS = 4  # rotating GEMM operand sets: 4 x 92-176 MB, beyond the 256 MB MALL
 
 
 def config5_inputs(torch):
@@ -354,9 +355,24 @@ def config5_operands(torch, dev):
     return (M, K, N), (X, W, dY), q
 
 
-def config5_gemms(torch, dev, q, dims):
+def quant_copy(r):
+    """The same QuantResult in storage of its own (same bytes, same strides)."""
+    import torch
+    from practice_cuda_amd.registry import QuantResult
+
+    def like(t):
+        c = torch.empty_strided(t.shape, t.stride(), dtype=t.dtype, device=t.device)
+        c.copy_(t)
+        return c
+    return QuantResult(like(r.tensor), like(r.dequant_scale), r.impl, r.granularity, dict(r.meta))
+
+
+def config5_gemms(torch, dev, q, dims, nsets=1):
     """The trio (fwd X W^T a_k_b_k, dgrad dY W a_k_b_n, wgrad dY^T X a_m_b_n
-    with the 128x1 requant) as launch closures over preallocated outputs."""
+    with the 128x1 requant) as launch closures over preallocated outputs;
+    launch(i) uses operand set i % nsets (set 0 is q, the others copies of
+    it in storage of their own, so that nsets > 2 keeps the operands from
+    staying in the 256 MB MALL between launches)."""
     from practice_cuda_amd.impls.hip_per_block import hip_per_block_bmm
     from practice_cuda_amd.registry import QuantResult
     M, K, N = dims
@@ -366,29 +382,30 @@ def config5_gemms(torch, dev, q, dims):
         return QuantResult(r.tensor.transpose(-1, -2), r.dequant_scale.transpose(-1, -2), r.impl,
                            "block", {"block_m": bn, "block_n": bm})
 
-    qx, qw, qdy, qx_m = q["x"], q["w"], q["dy"], q["x_m"]
-    wt = tr(qw, 128, 128)         # B = W^T  [1, K, N], K-major     (fwd)
-    dyt = tr(q["dy_m"], 128, 1)   # A = dY^T [1, N, M], M-major     (wgrad), 1x128 over M
-    out_f = torch.empty(1, M, N, dtype=torch.bfloat16, device=dev)
-    out_d = torch.empty(1, M, K, dtype=torch.bfloat16, device=dev)
-    out_w = torch.empty(1, N, K, dtype=torch.bfloat16, device=dev)
+    sets = [q] + [{k: quant_copy(v) for k, v in q.items()} for _ in range(nsets - 1)]
+    ops = [{"x": s["x"], "wt": tr(s["w"], 128, 128), "w": s["w"], "dy": s["dy"],
+            "dyt": tr(s["dy_m"], 128, 1), "x_m": s["x_m"]} for s in sets]
+    out_f = [torch.empty(1, M, N, dtype=torch.bfloat16, device=dev) for _ in range(nsets)]
+    out_d = [torch.empty(1, M, K, dtype=torch.bfloat16, device=dev) for _ in range(nsets)]
+    out_w = [torch.empty(1, N, K, dtype=torch.bfloat16, device=dev) for _ in range(nsets)]
     gemms = {
-        "fwd_a_k_b_k": lambda i: hip_per_block_bmm(qx, wt, out=out_f),
-        "dgrad_a_k_b_n": lambda i: hip_per_block_bmm(qdy, qw, out=out_d),
-        "wgrad_a_m_b_n": lambda i: hip_per_block_bmm(dyt, qx_m, out=out_w),
+        "fwd_a_k_b_k": lambda i: hip_per_block_bmm(ops[i % nsets]["x"], ops[i % nsets]["wt"], out=out_f[i % nsets]),
+        "dgrad_a_k_b_n": lambda i: hip_per_block_bmm(ops[i % nsets]["dy"], ops[i % nsets]["w"], out=out_d[i % nsets]),
+        "wgrad_a_m_b_n": lambda i: hip_per_block_bmm(ops[i % nsets]["dyt"], ops[i % nsets]["x_m"],
+                                                     out=out_w[i % nsets]),
     }
-    return gemms, dyt, (out_f, out_d, out_w)
+    return gemms, ops, (out_f, out_d, out_w)
 
 
-def bench_config5(torch, steps, warmup, dev):
+def bench_config5(torch, steps, warmup, dev, nsets=CONFIG5_SETS):
     """FP8 training-linear GEMM trio at M=8192 K=4096 N=14336: fwd X W^T
-    (a_k_b_k), dgrad dY W (a_k_b_n), wgrad dY^T X (a_m_b_n, 128x1 requant)."""
+    (a_k_b_k), dgrad dY W (a_k_b_n), wgrad dY^T X (a_m_b_n, 128x1 requant),
+    each over nsets rotating operand sets (beyond the MALL)."""
     from practice_cuda_amd.impls.hip_per_block import hip_per_block_bmm
     from practice_cuda_amd.registry import QuantResult
     dims, (X, W, dY), q = config5_operands(torch, dev)
     M, K, N = dims
-    qx, qw, qdy, qdy_m, qx_m = q["x"], q["w"], q["dy"], q["dy_m"], q["x_m"]
-    gemms, dyt, (out_f, out_d, out_w) = config5_gemms(torch, dev, q, dims)
+    gemms, ops, (out_f, out_d, out_w) = config5_gemms(torch, dev, q, dims, nsets)
     flops = 2 * M * N * K
     res = {}
     for name, fn in gemms.items():
@@ -398,27 +415,35 @@ def bench_config5(torch, steps, warmup, dev):
     total_ms = sum(r["ms"] for r in res.values())
     # the training layer's wgrad: the same product on K-major operands (its
     # dual quantizer stores the 128x1 results transposed); not part of the trio
-    dyt_k = QuantResult(dyt.tensor.contiguous(), dyt.dequant_scale, dyt.impl, "block", dict(dyt.meta))
-    qx_mk = QuantResult(qx_m.tensor.transpose(-1, -2).contiguous().transpose(-1, -2), qx_m.dequant_scale,
-                        qx_m.impl, "block", dict(qx_m.meta))
-    ms, _ = graph_time(torch, lambda i: hip_per_block_bmm(dyt_k, qx_mk, out=out_w), steps, warmup)
+    lay = [(QuantResult(o["dyt"].tensor.contiguous(), o["dyt"].dequant_scale, o["dyt"].impl, "block",
+                        dict(o["dyt"].meta)),
+            QuantResult(o["x_m"].tensor.transpose(-1, -2).contiguous().transpose(-1, -2), o["x_m"].dequant_scale,
+                        o["x_m"].impl, "block", dict(o["x_m"].meta))) for o in ops]
+    ms, _ = graph_time(torch, lambda i: hip_per_block_bmm(*lay[i % nsets], out=out_w[i % nsets]), steps, warmup)
     t = flops / (ms * 1e-3) / 1e12
     res["wgrad_layer_a_k_b_k"] = {"ms": ms, "TFLOP/s": t, "frac_of_fp8_peak": t / FP8_PEAK_TFLOPS,
                                   "note": "not in the trio total"}
-    del dyt_k, qx_mk
+    del lay
     # the channel-scaled recipe (one scale per row of X and of W) on the forward shape
     from practice_cuda_amd.impls.hip_per_channel import hip_per_channel_bmm, hip_per_channel_quant
     cx = hip_per_channel_quant(X[None], channel_axis=-2)
     cw = hip_per_channel_quant(W[None], channel_axis=-2)
     cwt = QuantResult(cw.tensor.transpose(-1, -2), cw.dequant_scale, cw.impl, "channel",
                       {**cw.meta, "channel_axis": -1})
-    ms, _ = graph_time(torch, lambda i: hip_per_channel_bmm(cx, cwt, out=out_f), steps, warmup)
+    chan = [(cx, cwt)] + [(quant_copy(cx), quant_copy(cwt)) for _ in range(nsets - 1)]
+    ms, _ = graph_time(torch, lambda i: hip_per_channel_bmm(*chan[i % nsets], out=out_f[i % nsets]), steps, warmup)
     t = flops / (ms * 1e-3) / 1e12
     res["fwd_channel_a_k_b_k"] = {"ms": ms, "TFLOP/s": t, "frac_of_fp8_peak": t / FP8_PEAK_TFLOPS,
                                   "note": "channel scales (per-channel recipe); not in the trio total"}
-    del cx, cw, cwt
+    # the trio with one operand set, for comparison: its operands stay in the MALL
+    res_mall = {}
+    g1, _, _ = config5_gemms(torch, dev, q, dims, 1)
+    for name, fn in g1.items():
+        ms, _ = graph_time(torch, fn, steps, warmup)
+        res_mall[name] = ms
+    del g1, cx, cw, cwt, chan
     tflops = 3 * flops / (total_ms * 1e-3) / 1e12
-    del qx, qw, qdy, qdy_m, qx_m, dyt, out_f, out_d, out_w, gemms, q
+    del ops, out_f, out_d, out_w, gemms, q
     torch.cuda.empty_cache()
     # the layer step's quantization launches: X and dY each quantized 1x128
     # and 128x1 by one kernel, W 128x128
@@ -438,14 +463,21 @@ def bench_config5(torch, steps, warmup, dev):
             "mfma_busy": busy if all(v is not None for v in busy.values()) else None}
     return {"name": "config5_training_linear_m8192_k4096_n14336", "ms_per_step": total_ms,
             "value": tflops, "unit": "TFLOP/s", "frac_of_fp8_peak": tflops / FP8_PEAK_TFLOPS,
-            "gemms": res, "flops_per_step": 3 * flops, "roofline": roof, "quant": quants, "layer_step": layer}
+            "operand_sets": nsets, "gemms": res, "gemms_one_operand_set_ms": res_mall,
+            "flops_per_step": 3 * flops, "roofline": roof, "quant": quants, "layer_step": layer}
 
 
 def layer_step(torch, X, W, dY, steps, dev):
     """Forward + backward of Float8BMMLinear at the config-5 shape: three fp8
     quantization launches (X 1x128 + 128x1 in one kernel, W 128x128, dY
-    1x128 + 128x1 in one kernel) and the three GEMMs, eager (autograd), timed
-    with events."""
+    1x128 + 128x1 in one kernel) and the three GEMMs, eager (autograd).
+
+    Timed with events in blocks of five steps, alternating with blocks of the
+    same six launches issued without autograd (layer_sequence), so that both
+    see the same clocks; `ms` and `sequence_ms` are the medians over the
+    blocks. `per_op_ms`: each launch of the sequence bracketed by its own
+    events over `steps` steps, all recorded before one synchronize (the host
+    stays ahead of the GPU, so no launch waits for it)."""
     from practice_cuda_amd.modules import Float8BMMLinear
     layer = Float8BMMLinear(1, X.shape[1], W.shape[0], bias=False, device=dev, dtype=torch.bfloat16)
     with torch.no_grad():
@@ -458,18 +490,69 @@ def layer_step(torch, X, W, dY, steps, dev):
         xg.grad = None
         layer(xg).backward(dy)
 
+    seq, names = layer_sequence(torch, X, W, dY)
+
+    def block(fn, n=5):
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        for _ in range(n):
+            fn()
+        end.record()
+        torch.cuda.synchronize()
+        return start.elapsed_time(end) / n
+
     for _ in range(5):
         step()
+        seq()
     torch.cuda.synchronize()
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    start.record()
+    auto, bare = [], []
+    for _ in range(max(2, steps // 5)):
+        auto.append(block(step))
+        bare.append(block(seq))
+    evs = []
     for _ in range(steps):
-        step()
-    end.record()
+        ev = {n: (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for n in names}
+        seq(ev)
+        evs.append(ev)
     torch.cuda.synchronize()
-    return {"ms": start.elapsed_time(end) / steps,
+    per_op = {n: statistics.median(ev[n][0].elapsed_time(ev[n][1]) for ev in evs) for n in names}
+    return {"ms": statistics.median(auto), "sequence_ms": statistics.median(bare), "per_op_ms": per_op,
+            "per_op_sum_ms": sum(per_op.values()),
             "what": "Float8BMMLinear forward + backward, 3 quantization launches (X and dY each 1x128 + 128x1 "
-                    "in one kernel, W 128x128) + 3 GEMMs, eager"}
+                    "in one kernel, W 128x128) + 3 GEMMs, eager; sequence: the same launches without autograd"}
+
+
+def layer_sequence(torch, X, W, dY):
+    """The layer step's six launches in its own order: the custom ops its
+    autograd function calls, with the same arguments. Returns (seq, names):
+    seq(ev=None) issues them, recording ev[name] = (start, end) events around
+    each when given."""
+    ops = torch.ops.pcamd
+    f8, blk, eps = torch.float8_e4m3fn, 128, 1e-12
+    x, w, dy = X[None], W[None], dY[None]
+    names = ["quant_x_dual", "quant_w_128x128", "fwd_gemm", "quant_dy_dual", "dgrad_gemm", "wgrad_gemm"]
+
+    def seq(ev=None):
+        out = {}
+
+        def mark(name, fn):
+            if ev is not None:
+                ev[name][0].record()
+            out[name] = fn()
+            if ev is not None:
+                ev[name][1].record()
+        mark("quant_x_dual", lambda: ops.quant_block_dual(x, blk, f8, eps))
+        mark("quant_w_128x128", lambda: ops.quant_block(w, blk, blk, f8, eps))
+        qx, sx, qxm, sxm = out["quant_x_dual"]
+        qw, sw = out["quant_w_128x128"]
+        mark("fwd_gemm", lambda: ops.block_scaled_bmm(qx, sx, qw.transpose(-2, -1), sw.transpose(-2, -1), None,
+                                                      1, blk, blk, x.dtype))
+        mark("quant_dy_dual", lambda: ops.quant_block_dual(dy, blk, f8, eps))
+        qdy, sdy, qdt, sdt = out["quant_dy_dual"]
+        mark("dgrad_gemm", lambda: ops.block_scaled_bmm(qdy, sdy, qw, sw, None, 1, blk, blk, dy.dtype))
+        mark("wgrad_gemm", lambda: ops.block_scaled_bmm(qdt.transpose(-2, -1), sdt.transpose(-2, -1), qxm, sxm,
+                                                        None, 1, blk, 1, dy.dtype))
+    return seq, names
 
 
 # ---------------------------------------------------------------------------
@@ -731,7 +814,8 @@ def pmc_probe_bmm(torch, dev):
     del launch4
     torch.cuda.empty_cache()
     dims, _, q = config5_operands(torch, dev)
-    gemms, dyt, outs = config5_gemms(torch, dev, q, dims)
+    gemms, ops, outs = config5_gemms(torch, dev, q, dims)
+    dyt = ops[0]["dyt"]
     dyt_k = QuantResult(dyt.tensor.contiguous(), dyt.dequant_scale, dyt.impl, "block", dict(dyt.meta))
     qx_m = q["x_m"]
     qx_mk = QuantResult(qx_m.tensor.transpose(-1, -2).contiguous().transpose(-1, -2), qx_m.dequant_scale,

@@ -13,6 +13,8 @@
  *                          (launches kernels/quant/per_block.py:6-48)
  *   pcamd_quant_block_dual <- no single counterpart: the block_m = 1 and
  *                          block_n = 1 calls of pcamd_quant_block on one tensor
+ *   pcamd_quant_block_ex, pcamd_quant_block_dual_ex <- the two above with an
+ *                          output store policy (flags)
  *   pcamd_quant_channel <- fp8_training/fp8_bench/impls/triton_per_channel.py:90-219
  *                          (launches kernels/quant/per_channel.py:35-102, :105-267)
  *   pcamd_quant_tensor  <- fp8_training/fp8_bench/impls/triton_per_tensor.py:28-95
@@ -41,7 +43,7 @@
 extern "C" {
 #endif
 
-#define PCAMD_ABI_VERSION 2 /* 2: pcamd_bmm_scaled_mixed */
+#define PCAMD_ABI_VERSION 3 /* 2: pcamd_bmm_scaled_mixed; 3: pcamd_quant_block_ex, pcamd_quant_block_dual_ex */
 
 /* status codes */
 #define PCAMD_OK 0
@@ -60,6 +62,9 @@ extern "C" {
 #define PCAMD_SCALE_BLOCK 0   /* sa[b, m/qbm, k/qbk], sb[b, k/qbk, n/qbn] */
 #define PCAMD_SCALE_CHANNEL 1 /* sa[b, m], sb[b, n] */
 #define PCAMD_SCALE_TENSOR 2  /* sa[0] (and sb[0] when scales_are_quant) */
+
+/* quantizer flags (the _ex entry points) */
+#define PCAMD_QUANT_CACHED_OUTPUT 1 /* write y and the scales with ordinary, cache-allocating stores */
 
 /* BMM epilogue activations */
 #define PCAMD_ACT_NONE 0
@@ -108,6 +113,35 @@ int pcamd_quant_block_dual(const void *x, int x_dtype, int64_t batch,
                            float *scale_col, int64_t scb, int64_t scm,
                            int64_t scn, int64_t block, float fp8_max, float eps,
                            void *stream);
+
+/*
+ * pcamd_quant_block and pcamd_quant_block_dual with flags. By default the
+ * quantizers write their fp8 outputs and scales with non-temporal stores
+ * (the fastest for a quantization on its own); PCAMD_QUANT_CACHED_OUTPUT
+ * writes them with ordinary stores, which leave them in the GPU's caches
+ * (the 256 MB memory-side cache included) for a kernel that reads them next,
+ * e.g. the GEMM after the training layer's quantization. Bytes and scales
+ * are the same either way; flags = 0 is exactly the call without _ex; other
+ * bits return PCAMD_ERR_INVALID. The reference interfaces are those of
+ * pcamd_quant_block / pcamd_quant_block_dual (the Triton kernels there pick
+ * their own cache policy). Available from PCAMD_ABI_VERSION 3.
+ */
+int pcamd_quant_block_ex(const void *x, int x_dtype, int64_t batch, int64_t m,
+                         int64_t n, int64_t sxb, int64_t sxm, int64_t sxn,
+                         void *y, int y_dtype, int64_t syb, int64_t sym,
+                         int64_t syn, float *scale, int64_t ssb, int64_t ssm,
+                         int64_t ssn, int64_t block_m, int64_t block_n,
+                         float fp8_max, float eps, int flags, void *stream);
+int pcamd_quant_block_dual_ex(const void *x, int x_dtype, int64_t batch,
+                              int64_t m, int64_t n, int64_t sxb, int64_t sxm,
+                              int64_t sxn, void *y_row, int64_t syb,
+                              int64_t sym, int64_t syn, void *y_col,
+                              int64_t ycb, int64_t ycm, int64_t ycn,
+                              int y_dtype, float *scale_row, int64_t srb,
+                              int64_t srm, int64_t srn, float *scale_col,
+                              int64_t scb, int64_t scm, int64_t scn,
+                              int64_t block, float fp8_max, float eps,
+                              int flags, void *stream);
 
 /*
  * Per-channel quantization. channel_axis = -2: one scale per row (reduce over

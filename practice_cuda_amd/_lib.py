@@ -19,6 +19,7 @@ _LOCK = threading.Lock()
 _LIB = None
 
 F32, BF16, F16, E4M3FN, E5M2 = 0, 1, 2, 3, 4
+QUANT_CACHED_OUTPUT = 1  # quantizer flag: outputs with cache-allocating stores
 SCALE_BLOCK, SCALE_CHANNEL, SCALE_TENSOR = 0, 1, 2
 ACT_NONE, ACT_GELU = 0, 1
 # status codes (include/pcamd_fp8.h)
@@ -37,6 +38,8 @@ EXPORTED_SYMBOLS = (
     "pcamd_last_error",
     "pcamd_quant_block",
     "pcamd_quant_block_dual",
+    "pcamd_quant_block_ex",
+    "pcamd_quant_block_dual_ex",
     "pcamd_quant_channel",
     "pcamd_quant_tensor",
     "pcamd_bmm_scaled",
@@ -69,6 +72,12 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.pcamd_quant_block_dual.argtypes = (
         [_ptr, _int, _i64, _i64, _i64, _i64, _i64, _i64] + [_ptr, _i64, _i64, _i64] * 2 + [_int]
         + [_ptr, _i64, _i64, _i64] * 2 + [_i64, _flt, _flt, _ptr])
+    lib.pcamd_quant_block_ex.restype = _int
+    lib.pcamd_quant_block_ex.argtypes = (quant_head + [_ptr, _i64, _i64, _i64, _i64, _i64, _flt, _flt, _int, _ptr])
+    lib.pcamd_quant_block_dual_ex.restype = _int
+    lib.pcamd_quant_block_dual_ex.argtypes = (
+        [_ptr, _int, _i64, _i64, _i64, _i64, _i64, _i64] + [_ptr, _i64, _i64, _i64] * 2 + [_int]
+        + [_ptr, _i64, _i64, _i64] * 2 + [_i64, _flt, _flt, _int, _ptr])
     lib.pcamd_quant_channel.restype = _int
     lib.pcamd_quant_channel.argtypes = quant_head + [_ptr, _i64, _i64, _int, _flt, _flt, _ptr]
     lib.pcamd_quant_tensor.restype = _int

@@ -1140,14 +1140,28 @@ int dispatch_dt_fmt(int dt, int fmt, Args&&... args) {
 }
 
 // Quantized outputs are written once and not re-read by this kernel:
-// non-temporal stores measured 3-6% faster on MI355X. PCAMD_QUANT_NT=0
-// selects ordinary stores.
+// non-temporal stores measured 3-6% faster on MI355X for a quantization on
+// its own. A caller whose next kernel reads the outputs (the training
+// layer's GEMMs) asks for ordinary stores with PCAMD_QUANT_CACHED_OUTPUT
+// (the _ex entry points), which leave them in the 256 MB MALL: the
+// config-5 layer step 1601 -> 1533 us, its forward GEMM 437 -> 414 us.
+// The policy of the current call lives in a thread-local that the _ex entry
+// points set for the duration of the call (calls on other threads keep
+// their own). PCAMD_QUANT_NT=0 selects ordinary stores everywhere.
+thread_local bool tl_cached_output = false;
+
+struct CachedOutputScope {
+  bool saved;
+  explicit CachedOutputScope(bool on) : saved(tl_cached_output) { tl_cached_output = on; }
+  ~CachedOutputScope() { tl_cached_output = saved; }
+};
+
 inline bool nt_stores() {
   static const int v = [] {
     const char* e = getenv("PCAMD_QUANT_NT");
     return e && e[0] == '0' ? 0 : 1;
   }();
-  return v != 0;
+  return v != 0 && !tl_cached_output;
 }
 
 // The clamp of the reference (tl.clamp before the cast) is left out of the
@@ -1573,6 +1587,36 @@ extern "C" int pcamd_quant_block_dual(const void* x, int x_dtype, int64_t batch,
   if (rc) return rc;
   return pcamd_quant_block(x, x_dtype, batch, m, n, sxb, sxm, sxn, y_col, y_dtype, ycb, ycm, ycn, scale_col,
                            scb, scm, scn, block, 1, fp8_max, eps, stream);
+}
+
+extern "C" int pcamd_quant_block_ex(const void* x, int x_dtype, int64_t batch, int64_t m, int64_t n,
+                                    int64_t sxb, int64_t sxm, int64_t sxn, void* y, int y_dtype, int64_t syb,
+                                    int64_t sym, int64_t syn, float* scale, int64_t ssb, int64_t ssm, int64_t ssn,
+                                    int64_t block_m, int64_t block_n, float fp8_max, float eps, int flags,
+                                    void* stream) {
+  if (flags & ~PCAMD_QUANT_CACHED_OUTPUT) {
+    clear_error();
+    return set_error(PCAMD_ERR_INVALID, "unknown quantizer flags 0x%x", flags);
+  }
+  CachedOutputScope scope((flags & PCAMD_QUANT_CACHED_OUTPUT) != 0);
+  return pcamd_quant_block(x, x_dtype, batch, m, n, sxb, sxm, sxn, y, y_dtype, syb, sym, syn, scale, ssb, ssm,
+                           ssn, block_m, block_n, fp8_max, eps, stream);
+}
+
+extern "C" int pcamd_quant_block_dual_ex(const void* x, int x_dtype, int64_t batch, int64_t m, int64_t n,
+                                         int64_t sxb, int64_t sxm, int64_t sxn, void* y_row, int64_t syb,
+                                         int64_t sym, int64_t syn, void* y_col, int64_t ycb, int64_t ycm,
+                                         int64_t ycn, int y_dtype, float* scale_row, int64_t srb, int64_t srm,
+                                         int64_t srn, float* scale_col, int64_t scb, int64_t scm, int64_t scn,
+                                         int64_t block, float fp8_max, float eps, int flags, void* stream) {
+  if (flags & ~PCAMD_QUANT_CACHED_OUTPUT) {
+    clear_error();
+    return set_error(PCAMD_ERR_INVALID, "unknown quantizer flags 0x%x", flags);
+  }
+  CachedOutputScope scope((flags & PCAMD_QUANT_CACHED_OUTPUT) != 0);
+  return pcamd_quant_block_dual(x, x_dtype, batch, m, n, sxb, sxm, sxn, y_row, syb, sym, syn, y_col, ycb, ycm,
+                                ycn, y_dtype, scale_row, srb, srm, srn, scale_col, scb, scm, scn, block, fp8_max,
+                                eps, stream);
 }
 
 extern "C" int pcamd_quant_channel(const void* x, int x_dtype, int64_t batch, int64_t m, int64_t n,

@@ -32,8 +32,14 @@ def hip_per_block_quant(
     fp8_dtype: torch.dtype = torch.float8_e4m3fn,
     eps: float = 1e-12,
     profile: bool = False,
+    cache_outputs: bool = False,
 ) -> QuantResult:
-    """One fp32 dequant scale per block_m x block_n tile of the last two dims."""
+    """One fp32 dequant scale per block_m x block_n tile of the last two dims.
+
+    cache_outputs: write the fp8 tensor and scales with cache-allocating
+    stores (PCAMD_QUANT_CACHED_OUTPUT) for a GEMM that reads them next; the
+    default non-temporal stores are faster for a quantization on its own.
+    Same bytes either way."""
     del profile
     if x.ndim not in (2, 3):
         raise ValueError(f"per-block quant expects a 2D or 3D tensor, got {tuple(x.shape)}")
@@ -52,12 +58,12 @@ def hip_per_block_quant(
 
     L = _lib.lib()
     with torch.cuda.device(x.device):
-        rc = L.pcamd_quant_block(
+        rc = L.pcamd_quant_block_ex(
             _lib.ptr(x), _lib.dtype_code(x.dtype), batch, m, n, *xs,
             _lib.ptr(output), _lib.dtype_code(fp8_dtype), *ys,
             _lib.ptr(scale_storage), *scale_storage.stride(),
             block_m, block_n, float(torch.finfo(fp8_dtype).max), float(eps),
-            _lib.stream_of(x))
+            _lib.QUANT_CACHED_OUTPUT if cache_outputs else 0, _lib.stream_of(x))
     _lib.check(rc, "pcamd_quant_block")
 
     dequant_scale = scale_storage.squeeze(0) if x.ndim == 2 else scale_storage
@@ -82,6 +88,7 @@ def hip_per_block_quant_dual(
     fp8_dtype: torch.dtype = torch.float8_e4m3fn,
     eps: float = 1e-12,
     col_transposed: bool = False,
+    cache_outputs: bool = False,
 ) -> tuple[QuantResult, QuantResult]:
     """``(hip_per_block_quant(x, block_m=1, block_n=block), hip_per_block_quant(x,
     block_m=block, block_n=1))`` from one read of x.
@@ -94,6 +101,7 @@ def hip_per_block_quant_dual(
     buffer seen as [.., M, N]), so a GEMM that reduces over M reads it
     K-major; its rows are padded to a multiple of 16 bytes (row pitch
     ceil(M / 16) * 16), which the kernel's 16-byte transposed stores need.
+    cache_outputs: as for hip_per_block_quant.
     """
     if x.ndim not in (2, 3):
         raise ValueError(f"per-block quant expects a 2D or 3D tensor, got {tuple(x.shape)}")
@@ -116,11 +124,12 @@ def hip_per_block_quant_dual(
 
     L = _lib.lib()
     with torch.cuda.device(x.device):
-        rc = L.pcamd_quant_block_dual(
+        rc = L.pcamd_quant_block_dual_ex(
             _lib.ptr(x), _lib.dtype_code(x.dtype), batch, m, n, *xs,
             _lib.ptr(out_row), *ys, _lib.ptr(out_col), *yc, _lib.dtype_code(fp8_dtype),
             _lib.ptr(s_row), *s_row.stride(), _lib.ptr(s_col), *s_col.stride(),
-            block, float(torch.finfo(fp8_dtype).max), float(eps), _lib.stream_of(x))
+            block, float(torch.finfo(fp8_dtype).max), float(eps),
+            _lib.QUANT_CACHED_OUTPUT if cache_outputs else 0, _lib.stream_of(x))
     _lib.check(rc, "pcamd_quant_block_dual")
 
     def result(q, s, bm, bn):

@@ -124,8 +124,10 @@ def _(a, b, scale, bias, out_dtype):
 @torch.library.custom_op("pcamd::quant_block", mutates_args=())
 def quant_block(x: torch.Tensor, block_m: int, block_n: int, fp8_dtype: torch.dtype,
                 eps: float) -> tuple[torch.Tensor, torch.Tensor]:
-    """(fp8 [B,M,N], fp32 dequant scales [B, ceil(M/block_m), ceil(N/block_n)])."""
-    q = hip_per_block_quant(x, block_m=block_m, block_n=block_n, fp8_dtype=fp8_dtype, eps=eps)
+    """(fp8 [B,M,N], fp32 dequant scales [B, ceil(M/block_m), ceil(N/block_n)]),
+    written with cache-allocating stores: the layer's GEMM reads them next."""
+    q = hip_per_block_quant(x, block_m=block_m, block_n=block_n, fp8_dtype=fp8_dtype, eps=eps,
+                            cache_outputs=True)
     return q.tensor, q.dequant_scale
 
 
@@ -143,8 +145,9 @@ def quant_block_dual(x: torch.Tensor, block: int, fp8_dtype: torch.dtype,
     of x: (fp8 1 x block, its scales [B, M, ceil(N/block)], fp8 block x 1 stored
     transposed (a [B, N, M] buffer with rows padded to 16 bytes, seen as
     [B, M, N]: the K-major operand of a GEMM reducing over M), its scales
-    [B, ceil(M/block), N])."""
-    r, c = hip_per_block_quant_dual(x, block=block, fp8_dtype=fp8_dtype, eps=eps, col_transposed=True)
+    [B, ceil(M/block), N]); cache-allocating stores, as for quant_block."""
+    r, c = hip_per_block_quant_dual(x, block=block, fp8_dtype=fp8_dtype, eps=eps, col_transposed=True,
+                                    cache_outputs=True)
     return r.tensor, r.dequant_scale, c.tensor, c.dequant_scale
 
 

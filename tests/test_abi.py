@@ -72,6 +72,23 @@ def test_invalid_arguments_are_rejected():
     assert rc == -1 and b"channel_axis" in L.pcamd_last_error()
 
 
+def test_quant_ex_flags_are_checked():
+    L = _lib.lib()
+    head = (FAKE, _lib.BF16, 1, 4, 256, 0, 256, 1)
+    rc = L.pcamd_quant_block_ex(*head, FAKE, _lib.E4M3FN, 0, 256, 1, FAKE, 0, 2, 1, 1, 128, 448.0, 1e-12, 2, None)
+    assert rc == -1 and b"flags" in L.pcamd_last_error()
+    rc = L.pcamd_quant_block_dual_ex(*head, FAKE, 0, 256, 1, FAKE, 0, 256, 1, _lib.E4M3FN, FAKE, 0, 2, 1,
+                                     FAKE, 0, 256, 1, 128, 448.0, 1e-12, 4, None)
+    assert rc == -1 and b"flags" in L.pcamd_last_error()
+    # a valid flag reaches the same validation as the call without _ex
+    rc = L.pcamd_quant_block_ex(*head, FAKE, _lib.E4M3FN, 0, 256, 1, FAKE, 0, 2, 1, 3, 128, 448.0, 1e-12,
+                                _lib.QUANT_CACHED_OUTPUT, None)
+    assert rc == -1 and b"powers of two" in L.pcamd_last_error()
+    rc = L.pcamd_quant_block_ex(*head[:3], 0, *head[4:], FAKE, _lib.E4M3FN, 0, 256, 1, FAKE, 0, 2, 1, 1, 128,
+                                448.0, 1e-12, _lib.QUANT_CACHED_OUTPUT, None)
+    assert rc == 0 and L.pcamd_last_error() == b""
+
+
 def _bmm(**over):
     args = dict(a=FAKE, b=FAKE, abd=_lib.E4M3FN, B=1, M=128, N=128, K=128,
                 sab=0, sam=128, sak=1, sbb=0, sbk=128, sbn=1, c=FAKE, cd=_lib.BF16,
