@@ -714,6 +714,15 @@ inline bool transposed_disabled() {
   return off;
 }
 
+// PCAMD_BMM_HALVES=0 keeps whole 256 x 256 tiles for small grids (read once)
+inline bool halves_disabled() {
+  static const bool off = [] {
+    const char* e = getenv("PCAMD_BMM_HALVES");
+    return e && e[0] == '0';
+  }();
+  return off;
+}
+
 template <bool A_K, bool B_K, int FA, int FB, int MODE, int SBK, int JN, bool KT, bool CT = false>
 int launch_tiles(const FastArgs& a, int grid, hipStream_t st) {
   auto kern = bmm_wide_kernel<A_K, B_K, FA, FB, MODE, SBK, JN, KT, CT>;
@@ -726,10 +735,16 @@ int launch_tiles(const FastArgs& a, int grid, hipStream_t st) {
 
 // One workgroup per tile (one per CU at a time: the LDS stages allow no
 // more). When the last wave of tiles would occupy at most half the CUs, it
-// runs as a second launch of half tiles instead.
+// runs as a second launch of half tiles instead; a grid of at most half as
+// many tiles as CUs runs as half tiles altogether (twice the CUs at work).
 template <bool A_K, bool B_K, int FA, int FB, int MODE, int SBK, bool KT>
 int launch_one(const FastArgs& a, hipStream_t st) {
   const int cus = device_cu_count(st);
+  if (cus > 0 && 2 * a.total_tiles <= cus && !halves_disabled()) {
+    FastArgs half = a;
+    half.tile_base = 0;
+    return launch_tiles<A_K, B_K, FA, FB, MODE, SBK, 4, KT>(half, 2 * a.total_tiles, st);
+  }
   const int tail = cus > 0 && a.total_tiles > cus ? a.total_tiles % cus : 0;
   if (tail == 0 || 2 * tail > cus) return launch_tiles<A_K, B_K, FA, FB, MODE, SBK, 8, KT>(a, a.total_tiles, st);
   FastArgs whole = a;
