@@ -19,7 +19,7 @@ BUILD_DIR = os.path.join(PKG_DIR, "_build")
 LIB_NAME = "libpcamd_fp8.so"
 LIB_PATH = os.path.join(BUILD_DIR, LIB_NAME)
 SOURCES = ["abi.hip", "quant.hip", "bmm.hip", "bmm_fast.hip", "bmm_wide.hip", "bmm_wide_e5m2.hip",
-           "bmm_wide_e5m2_e4m3.hip", "bmm_wide_e4m3_e5m2.hip", "bmm_stream.hip", "repack.hip"]
+           "bmm_wide_e5m2_e4m3.hip", "bmm_wide_e4m3_e5m2.hip", "bmm_stream.hip", "bmm_fused_stream.hip", "repack.hip"]
 
 ARCH = os.environ.get("PCAMD_OFFLOAD_ARCH", "gfx950")
 

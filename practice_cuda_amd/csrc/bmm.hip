@@ -611,6 +611,15 @@ extern "C" int pcamd_bmm_scaled_mixed(const void* a, int a_dtype, const void* b,
 // groups along K, the quantizer's exact bytes and scales); see
 // include/pcamd_fp8.h. Layouts outside the fused kernel's envelope return
 // PCAMD_ERR_UNSUPPORTED so the caller can quantize and multiply separately.
+// PCAMD_BMM_FUSED_STREAM=0: narrow fused products take the 128 x 256 kernel too (read once)
+static bool fused_stream_disabled() {
+  static const bool off = [] {
+    const char* e = getenv("PCAMD_BMM_FUSED_STREAM");
+    return e && e[0] == '0';
+  }();
+  return off;
+}
+
 extern "C" int pcamd_bmm_quant_a(const void* a, int a_dtype, const void* b, int ab_dtype, int64_t batch,
                                  int64_t m, int64_t n, int64_t k, int64_t sab, int64_t sam, int64_t sak,
                                  int64_t sbb, int64_t sbk, int64_t sbn, void* c, int c_dtype, int64_t scb,
@@ -676,5 +685,9 @@ extern "C" int pcamd_bmm_quant_a(const void* a, int a_dtype, const void* b, int 
   f.qa_out = static_cast<uint8_t*>(qa_out); f.sa_out = sa_out;
   f.sqab = sqab; f.sqam = sqam; f.soab = soab; f.soam = soam; f.soak = soak;
   f.fp8_max = fp8_max; f.eps = eps;
+  // narrow products stream A once (the 128 x 256 kernel quantizes each A
+  // row block once per N tile and runs few tiles)
+  if (bmm_fused_stream_ok(f, batch, qbn) && !fused_stream_disabled())
+    return bmm_fused_stream_launch(f, a_dtype, ab_dtype, b_k, batch, static_cast<hipStream_t>(stream));
   return bmm_fused_launch(f, a_dtype, ab_dtype, b_k, qbn < 16, static_cast<hipStream_t>(stream));
 }

@@ -50,6 +50,12 @@ int bmm_fast_tile_n();
 // of B and of the quantized A
 int bmm_fused_launch(const FastArgs& a, int a_dtype, int fmt, bool b_k, bool sb_col, hipStream_t st);
 
+// the same product for narrow N (bmm_fused_stream.hip): A streamed once,
+// quantized in registers; bmm_fused_stream_ok is its envelope (N <= 256,
+// N % 16 == 0, K % 256 == 0, qbn >= 128, plain 16-bit output)
+bool bmm_fused_stream_ok(const FastArgs& a, int64_t batch, int64_t qbn);
+int bmm_fused_stream_launch(const FastArgs& a, int a_dtype, int fmt, bool b_k, int64_t batch, hipStream_t st);
+
 // persistent streaming kernel for K == 128, N == 512, A K-major, B N-major,
 // 1 x 128 A scales and column-block B scales, plain bf16 output
 // (bmm_stream.hip); bmm_stream_ok is the host-side envelope check

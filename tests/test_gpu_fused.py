@@ -45,6 +45,12 @@ CASES = [
     (2, 384, 256, 384, torch.bfloat16, torch.float8_e5m2, 128, False),
     (1, 136, 264, 640, torch.float16, torch.float8_e4m3fn, 32, True),       # ragged M and N, 128x32 B blocks
     (2, 128, 256, 256, torch.bfloat16, torch.float8_e4m3fn, 1, False),      # 128x1 B blocks
+    # narrow products (N <= 256, K % 256 == 0, qbn >= 128): the streaming kernel
+    (2, 300, 256, 1024, torch.bfloat16, torch.float8_e4m3fn, 128, True),    # ragged M, 8 K steps
+    (1, 128, 128, 512, torch.float16, torch.float8_e4m3fn, 128, False),     # N 128, N-major B
+    (2, 512, 192, 768, torch.bfloat16, torch.float8_e5m2, 256, False),      # N 192 (partial stage), 256-wide B blocks
+    (1, 1000, 64, 256, torch.bfloat16, torch.float8_e4m3fn, 128, True),     # N 64, two K steps
+    (1, 2048, 256, 4096, torch.bfloat16, torch.float8_e4m3fn, 128, False),  # 32 K steps
 ]
 
 
@@ -72,6 +78,22 @@ def test_fused_matches_quantizer_and_unfused(dev, case):
     # without the write-out the product is the same
     out2 = hip_per_block_bmm_quant_a(x, qb)
     assert torch.equal(out, out2)
+
+
+@pytest.mark.parametrize("n", [256, 512])
+def test_fused_clamped_instantiation(dev, n):
+    # eps = 1e-40 makes fp8_max / eps overflow, so the kernels keep the clamp
+    # before the cast (N 256: the streaming kernel; N 512: the tiled one)
+    print(f"fused quant bmm clamp n={n}", flush=True)
+    x = _rand((1, 256, 512), 13).to(dev)
+    qb = _b_operand(1, 512, n, 14, dev)
+    out, qa = hip_per_block_bmm_quant_a(x, qb, eps=1e-40, return_quant=True)
+    ref_q = hip_per_block_quant(x, block_m=1, block_n=128, eps=1e-40)
+    unfused = hip_per_block_bmm(ref_q, qb)
+    torch.cuda.synchronize()
+    assert torch.equal(qa.tensor.view(torch.uint8), ref_q.tensor.view(torch.uint8))
+    assert torch.equal(qa.dequant_scale.view(torch.int32), ref_q.dequant_scale.view(torch.int32))
+    assert (out.float() - unfused.float()).abs().max().item() <= 1e-6 * unfused.float().abs().max().item()
 
 
 @pytest.mark.parametrize("activation", ["none", "gelu"])
