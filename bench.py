@@ -1040,9 +1040,10 @@ def fused_probe(torch, dev, steps, warmup):
     timed on the same inputs: bf16 A [M, K], e4m3 B [K, N] (N-major,
     128x128 scales), bf16 C. The fused kernel quantizes each A row block once
     per N tile, so it wins where few N tiles share A (small N) and loses as N
-    grows."""
-    from practice_cuda_amd.impls.hip_per_block import (hip_per_block_bmm, hip_per_block_bmm_quant_a,
-                                                       hip_per_block_quant)
+    grows; `default_path` names what hip_per_block_bmm_quant_a runs without
+    always_fused (the fused kernel up to FUSED_MAX_N columns)."""
+    from practice_cuda_amd.impls.hip_per_block import (FUSED_MAX_N, hip_per_block_bmm,
+                                                       hip_per_block_bmm_quant_a, hip_per_block_quant)
     g = torch.Generator(device=dev).manual_seed(0)
     rows = []
     for m, k, n in [(32768, 4096, 128), (32768, 4096, 256), (16384, 4096, 512), (8192, 4096, 1024),
@@ -1051,7 +1052,8 @@ def fused_probe(torch, dev, steps, warmup):
         qb = hip_per_block_quant((torch.randn(1, k, n, generator=g, device=dev) * 0.02).bfloat16(),
                                  block_m=128, block_n=128)
         out = torch.empty(1, m, n, device=dev, dtype=torch.bfloat16)
-        fused_ms, _ = graph_time(torch, lambda i: hip_per_block_bmm_quant_a(x, qb, out=out), steps, warmup)
+        fused_ms, _ = graph_time(torch, lambda i: hip_per_block_bmm_quant_a(x, qb, out=out, always_fused=True),
+                                 steps, warmup)
 
         def unfused(i):
             hip_per_block_bmm(hip_per_block_quant(x, block_m=1, block_n=128), qb, out=out)
@@ -1059,7 +1061,8 @@ def fused_probe(torch, dev, steps, warmup):
         unfused_ms, _ = graph_time(torch, unfused, steps, warmup)
         rows.append({"m": m, "k": k, "n": n, "fused_us": round(fused_ms * 1e3, 1),
                      "quantize_then_multiply_us": round(unfused_ms * 1e3, 1),
-                     "fused_speedup": round(unfused_ms / fused_ms, 3)})
+                     "fused_speedup": round(unfused_ms / fused_ms, 3),
+                     "default_path": "fused" if n <= FUSED_MAX_N else "quantize_then_multiply"})
         print(rows[-1], file=sys.stderr, flush=True)
         del x, qb, out
         torch.cuda.empty_cache()

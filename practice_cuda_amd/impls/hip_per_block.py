@@ -214,6 +214,10 @@ def hip_per_block_bmm(
 
 
 
+# widest product hip_per_block_bmm_quant_a sends to the fused kernel by default
+FUSED_MAX_N = 256
+
+
 def hip_per_block_bmm_quant_a(
     x: torch.Tensor,
     b: QuantResult,
@@ -224,6 +228,7 @@ def hip_per_block_bmm_quant_a(
     out: Optional[torch.Tensor] = None,
     activation: str = "none",
     return_quant: bool = False,
+    always_fused: bool = False,
 ):
     """``hip_per_block_bmm(hip_per_block_quant(x, block_m=1, block_n=128), b)``
     with the activation quantization inside the GEMM's K loop.
@@ -238,7 +243,11 @@ def hip_per_block_bmm_quant_a(
     (kernels/fp8_bmm/kernel/fp8_quant_bmm_fused_kernel.py:30-146, unfinished
     there), on the per-block recipe. Layouts the fused kernel does not cover
     (an M-major or unaligned x, K not a multiple of 128) take the two-kernel
-    path: hip_per_block_quant, then hip_per_block_bmm."""
+    path: hip_per_block_quant, then hip_per_block_bmm. So do products wider
+    than FUSED_MAX_N columns unless always_fused is set: the fused kernel
+    quantizes each A row block once per 256-column tile of C, and from two
+    tiles on the two-kernel path is faster (MI355X, M 16384, K 4096, N 512:
+    126 vs 91 us)."""
     if x.ndim not in (2, 3):
         raise ValueError(f"fused quant BMM expects a 2D or 3D activation, got {tuple(x.shape)}")
     if x.dtype not in (torch.bfloat16, torch.float16):
@@ -270,7 +279,7 @@ def hip_per_block_bmm_quant_a(
         sa = torch.empty((batch, m, -(-k // 128)), device=x3.device, dtype=torch.float32)
     L = _lib.lib()
     rc = _lib.ERR_UNSUPPORTED
-    if in_b in ("n-major", "k-major") and x3.stride(-1) == 1:
+    if in_b in ("n-major", "k-major") and x3.stride(-1) == 1 and (always_fused or n <= FUSED_MAX_N):
         with torch.cuda.device(x3.device):
             rc = L.pcamd_bmm_quant_a(
                 _lib.ptr(x3), _lib.dtype_code(x3.dtype), _lib.ptr(b.tensor), _lib.dtype_code(fp8_dtype),

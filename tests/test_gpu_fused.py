@@ -61,7 +61,7 @@ def test_fused_matches_quantizer_and_unfused(dev, case):
     print(f"fused quant bmm {case}", flush=True)
     x = _rand((bsz, m, k), 1, dtype=xdt).to(dev)
     qb = _b_operand(bsz, k, n, 2, dev, qbn=qbn, k_major=b_k, fmt=fmt)
-    out, qa = hip_per_block_bmm_quant_a(x, qb, return_quant=True)
+    out, qa = hip_per_block_bmm_quant_a(x, qb, return_quant=True, always_fused=True)
     torch.cuda.synchronize()
     ref_q = hip_per_block_quant(x, block_m=1, block_n=128, fp8_dtype=fmt)
     # the A the kernel quantized is the quantizer's, bit for bit
@@ -76,7 +76,7 @@ def test_fused_matches_quantizer_and_unfused(dev, case):
     ref = O.bmm_reference(ref_q.dequantize().double().cpu().numpy(), qb.dequantize().double().cpu().numpy())
     assert O.max_abs_rel(out.float().cpu().numpy(), ref) <= TOL
     # without the write-out the product is the same
-    out2 = hip_per_block_bmm_quant_a(x, qb)
+    out2 = hip_per_block_bmm_quant_a(x, qb, always_fused=True)
     assert torch.equal(out, out2)
 
 
@@ -87,7 +87,7 @@ def test_fused_clamped_instantiation(dev, n):
     print(f"fused quant bmm clamp n={n}", flush=True)
     x = _rand((1, 256, 512), 13).to(dev)
     qb = _b_operand(1, 512, n, 14, dev)
-    out, qa = hip_per_block_bmm_quant_a(x, qb, eps=1e-40, return_quant=True)
+    out, qa = hip_per_block_bmm_quant_a(x, qb, eps=1e-40, return_quant=True, always_fused=True)
     ref_q = hip_per_block_quant(x, block_m=1, block_n=128, eps=1e-40)
     unfused = hip_per_block_bmm(ref_q, qb)
     torch.cuda.synchronize()
@@ -128,6 +128,21 @@ def test_fused_falls_back_outside_envelope(dev, layout):
     assert torch.equal(qa.tensor.view(torch.uint8), ref_q.tensor.view(torch.uint8))
 
 
+def test_wide_products_take_two_kernel_path(dev):
+    # above FUSED_MAX_N columns the default call quantizes, then multiplies:
+    # the unfused results exactly, and the same quantization returned
+    x = _rand((1, 256, 512), 15).to(dev)
+    qb = _b_operand(1, 512, 512, 16, dev)
+    out, qa = hip_per_block_bmm_quant_a(x, qb, return_quant=True)
+    ref_q = hip_per_block_quant(x, block_m=1, block_n=128)
+    ref = hip_per_block_bmm(ref_q, qb)
+    fused = hip_per_block_bmm_quant_a(x, qb, always_fused=True)
+    torch.cuda.synchronize()
+    assert torch.equal(out, ref)
+    assert torch.equal(qa.tensor.view(torch.uint8), ref_q.tensor.view(torch.uint8))
+    assert (fused.float() - ref.float()).abs().max().item() <= 1e-6 * ref.float().abs().max().item()
+
+
 def test_fused_2d_activation(dev):
     x = _rand((256, 384), 8).to(dev)
     qb = _b_operand(1, 384, 256, 9, dev)
@@ -147,7 +162,7 @@ def test_fused_config4_shape(dev):
     bh = torch.randn(128, 128, 512, generator=g).bfloat16().to(dev)
     qb = hip_per_block_quant(bh, block_m=128, block_n=128)
     print("fused config4", flush=True)
-    out, qa = hip_per_block_bmm_quant_a(ah, qb, return_quant=True)
+    out, qa = hip_per_block_bmm_quant_a(ah, qb, return_quant=True, always_fused=True)
     ref_q = hip_per_block_quant(ah, block_m=1, block_n=128)
     assert torch.equal(qa.tensor.view(torch.uint8), ref_q.tensor.view(torch.uint8))
     ref = torch.bmm(ref_q.dequantize().contiguous(), qb.dequantize().contiguous())
