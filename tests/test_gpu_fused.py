@@ -51,6 +51,10 @@ CASES = [
     (2, 512, 192, 768, torch.bfloat16, torch.float8_e5m2, 256, False),      # N 192 (partial stage), 256-wide B blocks
     (1, 1000, 64, 256, torch.bfloat16, torch.float8_e4m3fn, 128, True),     # N 64, two K steps
     (1, 2048, 256, 4096, torch.bfloat16, torch.float8_e4m3fn, 128, False),  # 32 K steps
+    # N <= 128 with K % 512 == 0: two K blocks per pipeline step
+    (2, 300, 128, 2048, torch.bfloat16, torch.float8_e4m3fn, 128, True),    # ragged M, 8 steps
+    (1, 520, 96, 1536, torch.float16, torch.float8_e5m2, 128, False),       # N 96, 6 steps, N-major
+    (1, 256, 128, 768, torch.bfloat16, torch.float8_e4m3fn, 128, False),    # K % 512 != 0: one block per step
 ]
 
 
