@@ -43,7 +43,8 @@
 extern "C" {
 #endif
 
-#define PCAMD_ABI_VERSION 3 /* 2: pcamd_bmm_scaled_mixed; 3: pcamd_quant_block_ex, pcamd_quant_block_dual_ex */
+#define PCAMD_ABI_VERSION 4 /* 2: pcamd_bmm_scaled_mixed; 3: pcamd_quant_block_ex, pcamd_quant_block_dual_ex;
+                              4: PCAMD_F64 scale arithmetic of pcamd_quant_tensor */
 
 /* status codes */
 #define PCAMD_OK 0
@@ -57,6 +58,7 @@ extern "C" {
 #define PCAMD_F16 2
 #define PCAMD_E4M3FN 3 /* OCP fp8 e4m3fn: max 448, no inf, NaN = 0x7f/0xff */
 #define PCAMD_E5M2 4   /* OCP fp8 e5m2: max 57344, inf = 0x7c */
+#define PCAMD_F64 5    /* scale arithmetic only (pcamd_quant_tensor) */
 
 /* BMM scale modes */
 #define PCAMD_SCALE_BLOCK 0   /* sa[b, m/qbm, k/qbk], sb[b, k/qbk, n/qbn] */
@@ -166,7 +168,13 @@ int pcamd_quant_channel(const void *x, int x_dtype, int64_t batch, int64_t m,
  * fp8_training/fp8_bench/impls/triton_per_tensor.py:28-95; the input's dtype
  * for the legacy kernels/fp8_bmm/fp8_warper.py:9-77, whose torch ops on 0-d
  * tensors of the input's dtype round every step (the results are then
- * exactly representable in that dtype).
+ * exactly representable in that dtype). PCAMD_F64 (from PCAMD_ABI_VERSION 4)
+ * is torchao's tensorwise scale, which the reference's Float8BMMLinear
+ * quantizes with (fp8_training/fp8_bench/modules/float8/float8_utils.py:
+ * 45-48, used through float8_scaling_utils.py): qs = fp32(fp8_max /
+ * max(fp64(amax), eps)) with the division in fp64, scale[0] = reciprocal(qs)
+ * in fp32 (the reciprocal its scaled GEMMs take), then the same
+ * fp8_rne(clamp(x * qs)) (float8_training_tensor.py:153-154).
  */
 int pcamd_quant_tensor(const void *x, int x_dtype, int64_t batch, int64_t m,
                        int64_t n, int64_t sxb, int64_t sxm, int64_t sxn,

@@ -21,6 +21,10 @@
  *                         scale_dt = the input dtype the legacy
  *                         kernels/fp8_bmm/fp8_warper.py:21-25 +
  *                         kernel/fp8_quant_kernel.py:56-60
+ *                         and with scale_dt = OR_F64 torchao's tensorwise
+ *                         scale (fp8_training/fp8_bench/modules/float8/
+ *                         float8_utils.py:45-48 + float8_training_tensor.py:
+ *                         153-154), which the reference layer quantizes with
  *   oracle_round_dt:      the bf16 / fp16 rounding of torch's 0-d tensor ops
  *
  * Pinning (tests/test_oracle.py): the encoders against torch's CPU cast over
@@ -40,7 +44,7 @@
 #include <omp.h>
 #endif
 
-enum { OR_F32 = 0, OR_BF16 = 1, OR_F16 = 2, OR_E4M3 = 3, OR_E5M2 = 4 };
+enum { OR_F32 = 0, OR_BF16 = 1, OR_F16 = 2, OR_E4M3 = 3, OR_E5M2 = 4, OR_F64 = 5 };
 
 static inline float bits_to_f32(uint32_t u) {
   float f;
@@ -264,12 +268,21 @@ int oracle_quant_tensor(const void *x, int xd, int64_t batch, int64_t m, int64_t
         float a = fabsf(load_elem(x, xd, b * sxb + r * sxm + c * sxn));
         amax = fmaxf(amax, a);
       }
-  float safe = oracle_round_dt(fmaxf(oracle_round_dt(amax, scale_dt), oracle_round_dt(eps, scale_dt)), scale_dt);
-  /* `fp8_max / max_abs` with a Python-float numerator is evaluated by torch
-   * as max_abs.reciprocal() * fp8_max (torch/_tensor.py __rdiv__): two
-   * roundings, unlike the true division of the Triton kernels. */
-  float qs = oracle_round_dt(oracle_round_dt(1.0f / safe, scale_dt) * fp8_max, scale_dt);
-  float ds = oracle_round_dt(1.0f / qs, scale_dt); /* quant_scale.reciprocal() */
+  float qs, ds;
+  if (scale_dt == OR_F64) {
+    /* torchao amax_to_scale (float8_utils.py:45-48): amax.to(float64),
+     * max / clamp(amax, min=EPS) in fp64, .to(float32); its scaled GEMMs
+     * take scale.reciprocal() in fp32 */
+    qs = (float)((double)fp8_max / fmax((double)amax, (double)eps));
+    ds = 1.0f / qs;
+  } else {
+    float safe = oracle_round_dt(fmaxf(oracle_round_dt(amax, scale_dt), oracle_round_dt(eps, scale_dt)), scale_dt);
+    /* `fp8_max / max_abs` with a Python-float numerator is evaluated by torch
+     * as max_abs.reciprocal() * fp8_max (torch/_tensor.py __rdiv__): two
+     * roundings, unlike the true division of the Triton kernels. */
+    qs = oracle_round_dt(oracle_round_dt(1.0f / safe, scale_dt) * fp8_max, scale_dt);
+    ds = oracle_round_dt(1.0f / qs, scale_dt); /* quant_scale.reciprocal() */
+  }
   *scale = ds;
   if (quant_scale) *quant_scale = qs;
   for (int64_t b = 0; b < batch; ++b)

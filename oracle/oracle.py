@@ -33,6 +33,7 @@ _LIB_PATH = os.path.join(_HERE, "_build", "liboracle.so")
 _LIB = None
 
 F32, BF16, F16, E4M3, E5M2 = 0, 1, 2, 3, 4
+F64 = 5  # scale arithmetic only: torchao's tensorwise form
 FP8_MAX = {E4M3: 448.0, E5M2: 57344.0}
 _FMT_NAMES = {"e4m3": E4M3, "e4m3fn": E4M3, "e5m2": E5M2, E4M3: E4M3, E5M2: E5M2}
 _DT_NAMES = {"f32": F32, "fp32": F32, "float32": F32, "bf16": BF16, "bfloat16": BF16,
@@ -211,7 +212,9 @@ def quant_tensor(x, fmt="e4m3", eps: float = 1e-12, dtype: Optional[str] = None,
 
     scale_dt (F32 / BF16 / F16) is the dtype of the scale arithmetic: F32 for
     impls/triton_per_tensor.py, the input's dtype for the legacy
-    kernels/fp8_bmm/fp8_warper.py:21-25 (pass ``scale_dt="input"``).
+    kernels/fp8_bmm/fp8_warper.py:21-25 (pass ``scale_dt="input"``). F64 is
+    torchao's tensorwise scale (modules/float8/float8_utils.py:45-48):
+    qs = fp32(fp8_max / max(fp64(amax), eps)), dequant = fp32 reciprocal.
     fp8_max defaults to the format's largest finite value (the legacy API's
     fp8_range argument can override it).
     """

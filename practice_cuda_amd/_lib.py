@@ -19,6 +19,7 @@ _LOCK = threading.Lock()
 _LIB = None
 
 F32, BF16, F16, E4M3FN, E5M2 = 0, 1, 2, 3, 4
+F64 = 5  # scale arithmetic of pcamd_quant_tensor only (torchao's tensorwise form)
 QUANT_CACHED_OUTPUT = 1  # quantizer flag: outputs with cache-allocating stores
 SCALE_BLOCK, SCALE_CHANNEL, SCALE_TENSOR = 0, 1, 2
 ACT_NONE, ACT_GELU = 0, 1

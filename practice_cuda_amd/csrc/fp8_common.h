@@ -22,6 +22,7 @@ constexpr int kBF16 = PCAMD_BF16;
 constexpr int kF16 = PCAMD_F16;
 constexpr int kE4M3 = PCAMD_E4M3FN;
 constexpr int kE5M2 = PCAMD_E5M2;
+constexpr int kF64 = PCAMD_F64;  // scale arithmetic only
 
 // ---------------------------------------------------------------------------
 // element conversions
@@ -298,6 +299,7 @@ PCAMD_DEV uint32_t quant_one(float v, float qs, float fp8_max) {
 // per-block:   dequant = 1 / (fp8_max / max(amax, eps))
 // per-channel: dequant = max(amax, eps) / fp8_max
 // per-tensor:  dequant = 1 / ((1 / max(amax, eps)) * fp8_max)
+//   (torchao's tensorwise form, scale_dt kF64: dequant = 1 / fp32(fp8_max / max(amax, eps)) in fp64)
 struct Scales {
   float qs, ds;
 };
@@ -328,6 +330,12 @@ PCAMD_DEV float round_dt(float v, int dt) {
 // legacy kernels/fp8_bmm/fp8_warper.py:21-25 (each op evaluated in fp32, then
 // rounded to that dtype).
 PCAMD_DEV Scales tensor_scales(float amax, float fp8_max, float eps, int scale_dt = kF32) {
+  if (scale_dt == kF64) {
+    // torchao's amax_to_scale: the division in fp64, rounded once to fp32
+    const float qs = static_cast<float>(static_cast<double>(fp8_max) /
+                                        fmax(static_cast<double>(amax), static_cast<double>(eps)));
+    return {qs, 1.0f / qs};
+  }
   const float s = round_dt(fmaxf(round_dt(amax, scale_dt), round_dt(eps, scale_dt)), scale_dt);
   const float qs = round_dt(round_dt(1.0f / s, scale_dt) * fp8_max, scale_dt);
   return {qs, round_dt(1.0f / qs, scale_dt)};

@@ -581,7 +581,7 @@ struct TensorArgs {
   int64_t sxb, sxm, sxn, syb, sym, syn;
   int64_t total;       // batch * m * n
   float fp8_max, eps;
-  int scale_dt;        // dtype of the scalar scale arithmetic (kF32 / kBF16 / kF16)
+  int scale_dt;        // scalar scale arithmetic: kF32 / kBF16 / kF16 steps, or kF64 (torchao's form)
 };
 
 template <int DT>
@@ -1696,8 +1696,8 @@ extern "C" int pcamd_quant_tensor(const void* x, int x_dtype, int64_t batch, int
   int rc = validate_common(x, x_dtype, batch, m, n, y, y_dtype, scale, fp8_max);
   if (rc) return rc;
   if (!scale) return set_error(PCAMD_ERR_INVALID, "null scale pointer");
-  if (scale_dtype != kF32 && scale_dtype != kBF16 && scale_dtype != kF16)
-    return set_error(PCAMD_ERR_INVALID, "scale_dtype must be f32, bf16 or f16 (got %d)", scale_dtype);
+  if (scale_dtype != kF32 && scale_dtype != kBF16 && scale_dtype != kF16 && scale_dtype != kF64)
+    return set_error(PCAMD_ERR_INVALID, "scale_dtype must be f32, bf16, f16 or f64 (got %d)", scale_dtype);
   TensorArgs a{};
   a.x = static_cast<const char*>(x); a.y = static_cast<uint8_t*>(y); a.scale = scale;
   a.quant_scale = quant_scale_out;

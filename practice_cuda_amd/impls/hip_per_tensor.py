@@ -23,8 +23,12 @@ def quant_tensor_raw(x: torch.Tensor, fp8_dtype: torch.dtype, eps: float, *,
     """Launch the per-tensor kernels; returns (fp8 tensor, dequant scale, quant scale).
 
     scale_dtype is the dtype the scalar scale steps are rounded to (fp32 for
-    the fp8_bench path; the input's dtype for the legacy fp8_warper API).
-    fp8_max defaults to the fp8 format's largest finite value.
+    the fp8_bench path; the input's dtype for the legacy fp8_warper API), or
+    torch.float64 for torchao's tensorwise scale (reference
+    modules/float8/float8_utils.py:45-48: qs = fp32(fp8_max / max(fp64(amax),
+    eps)), dequant = its fp32 reciprocal), which the reference's training
+    layer quantizes with. fp8_max defaults to the fp8 format's largest finite
+    value.
     """
     output = torch.empty_like(x, dtype=fp8_dtype, memory_format=torch.preserve_format)
     batch, m, n, xs, ys = C.dims3(x, output)
@@ -37,7 +41,7 @@ def quant_tensor_raw(x: torch.Tensor, fp8_dtype: torch.dtype, eps: float, *,
             _lib.ptr(output), _lib.dtype_code(fp8_dtype), *ys,
             _lib.ptr(scales[0:1]), _lib.ptr(scales[1:2]),
             float(torch.finfo(fp8_dtype).max if fp8_max is None else fp8_max), float(eps),
-            _lib.dtype_code(scale_dtype), _lib.stream_of(x))
+            _lib.F64 if scale_dtype == torch.float64 else _lib.dtype_code(scale_dtype), _lib.stream_of(x))
     _lib.check(rc, "pcamd_quant_tensor")
     return output, scales[0], scales[1]
 

@@ -21,7 +21,10 @@ Every GEMM is ``pcamd::block_scaled_bmm``, a ``torch.library`` custom op over
 multiplied by sa * sb, kernels/bmm/per_block.py:99-111), so the layer also
 traces under ``torch.compile``. Quantization is the 1x128 / 128x128 / 128x1
 ``pcamd_quant_block`` kernel. A per-tensor variant (``granularity="tensor"``)
-uses the per-tensor quantizer and the scalar-scaled GEMM.
+uses the per-tensor quantizer with torchao's tensorwise scale, the form the
+reference layer quantizes with (modules/float8/float8_utils.py:45-48:
+qs = fp32(fp8_max / max(fp64(amax), 1e-12)), bytes fp8(clamp(x * qs)),
+float8_training_tensor.py:153-154), and the scalar-scaled GEMM.
 """
 from __future__ import annotations
 
@@ -161,8 +164,9 @@ def _(x, block, fp8_dtype, eps):
 
 @torch.library.custom_op("pcamd::quant_tensor", mutates_args=())
 def quant_tensor(x: torch.Tensor, fp8_dtype: torch.dtype, eps: float) -> tuple[torch.Tensor, torch.Tensor]:
-    """(fp8 tensor like x, fp32 dequant scale of shape [1])."""
-    q, dequant, _ = quant_tensor_raw(x, fp8_dtype, eps)
+    """(fp8 tensor like x, fp32 dequant scale of shape [1]) with torchao's
+    tensorwise scale (the division in fp64, rounded once to fp32)."""
+    q, dequant, _ = quant_tensor_raw(x, fp8_dtype, eps, scale_dtype=torch.float64)
     return q, dequant.reshape(1).clone()
 
 

@@ -5,7 +5,9 @@ The block recipe is checked GEMM by GEMM against the oracle: X 1x128, W
 the CPU by oracle.quant_block, dequantized, and multiplied in float64;
 forward, dgrad and wgrad must each be within max-abs-relative 1e-2 (the BMM
 bar). dbias is dY summed over M. The per-tensor recipe is checked the same
-way with oracle.quant_tensor. The layer also runs under torch.compile
+way with oracle.quant_tensor in torchao's tensorwise form (scale arithmetic
+in fp64, the reference layer's), and its quantization op byte for byte. The
+layer also runs under torch.compile
 (aot_eager) with the same results, and at the config-5 shape its outputs stay
 within the fp8 quantization error of an fp32 GEMM of the unquantized values.
 """
@@ -27,7 +29,7 @@ def _deq_block(x: torch.Tensor, bm: int, bn: int) -> np.ndarray:
 
 
 def _deq_tensor(x: torch.Tensor) -> np.ndarray:
-    q, ds, _ = O.quant_tensor(x.cpu())
+    q, ds, _ = O.quant_tensor(x.cpu(), scale_dt=O.F64)
     return O.decode(q).astype(np.float64) * np.float64(ds)
 
 
@@ -114,12 +116,28 @@ def test_tensor_recipe_e5m2_grads_match_oracle(dev):
     w = layer.weight.detach().cpu()
 
     def deq(t, fmt):
-        q, ds, _ = O.quant_tensor(t.cpu(), fmt)
+        q, ds, _ = O.quant_tensor(t.cpu(), fmt, scale_dt=O.F64)
         return O.decode(q, fmt).astype(np.float64) * np.float64(ds)
 
     assert O.max_abs_rel(dx.float().cpu().numpy(), np.matmul(deq(dy, "e5m2"), deq(w, "e4m3"))) <= 1e-2
     assert O.max_abs_rel(dw.float().cpu().numpy(),
                          np.matmul(np.swapaxes(deq(dy, "e5m2"), -1, -2), deq(x, "e4m3"))) <= 1e-2
+
+
+@pytest.mark.parametrize("fmt", [torch.float8_e4m3fn, torch.float8_e5m2])
+def test_tensor_recipe_quantization_is_torchao_form(dev, fmt):
+    # the layer's per-tensor op writes the bytes and scale of torchao's form
+    # (the reference layer's), not the fp32 reciprocal-multiply form: the
+    # planted amax is one where the two scales differ
+    x = (torch.randn(2, 96, 160, generator=torch.Generator().manual_seed(8)) * 0.05).bfloat16()
+    x[0, 3, 4] = 0.5234375
+    q, ds = torch.ops.pcamd.quant_tensor(x.to(dev), fmt, 1e-12)
+    torch.cuda.synchronize()
+    name = "e4m3" if fmt == torch.float8_e4m3fn else "e5m2"
+    q_ref, ds_ref, qs_ref = O.quant_tensor(x, name, scale_dt=O.F64)
+    assert np.array_equal(q.view(torch.uint8).cpu().numpy(), q_ref)
+    assert np.float32(ds.item()) == np.float32(ds_ref)
+    assert np.float32(O.quant_tensor(x, name)[2]) != np.float32(qs_ref)
 
 
 def test_tensor_recipe_gemms_match_oracle(dev):

@@ -20,7 +20,7 @@ from oracle import oracle as O
 from practice_cuda_amd import _lib
 from practice_cuda_amd.impls.hip_per_block import hip_per_block_quant
 from practice_cuda_amd.impls.hip_per_channel import hip_per_channel_quant
-from practice_cuda_amd.impls.hip_per_tensor import hip_per_tensor_quant
+from practice_cuda_amd.impls.hip_per_tensor import hip_per_tensor_quant, quant_tensor_raw
 
 pytestmark = pytest.mark.gpu
 GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
@@ -464,6 +464,29 @@ def test_tensor_quant_matches_oracle(dev, shape, dtype, fmt):
     q_ref, ds, _ = O.quant_tensor(x, fmt)
     assert r.dequant_scale.ndim == 0
     assert_same(r, q_ref, np.float32(ds), f"tensor {shape}")
+
+
+@pytest.mark.parametrize("shape,dtype,fmt,amax", [((3, 40, 72), "bf16", "e4m3", 0.5234375),
+                                                  ((2048, 512), "bf16", "e5m2", 0.5390625),
+                                                  ((14, 2048, 512), "f32", "e4m3", 3.0),
+                                                  ((64, 96), "f16", "e4m3", 0.0)])
+def test_tensor_quant_torchao_form(dev, shape, dtype, fmt, amax):
+    # scale arithmetic in fp64 (torchao's tensorwise scale, the reference
+    # layer's form): the kernels' bytes and scales against the oracle; at
+    # the bf16 amax values the fp32 form gives another scale
+    print(f"tensor torchao form {shape} {dtype} {fmt} amax={amax}", flush=True)
+    x = make_input(shape, dtype, seed=17, scale=0.05, outliers=0.0)
+    if amax == 0.0:
+        x = torch.zeros_like(x)
+    else:
+        x.view(-1)[len(x.view(-1)) // 3] = -amax
+    q, ds, qs = quant_tensor_raw(x.to(dev), FMT[fmt], 1e-12, scale_dtype=torch.float64)
+    q_ref, ds_ref, qs_ref = O.quant_tensor(x, fmt, scale_dt=O.F64)
+    torch.cuda.synchronize()
+    assert np.array_equal(qbits(q), q_ref)
+    assert np.float32(ds.item()) == np.float32(ds_ref) and np.float32(qs.item()) == np.float32(qs_ref)
+    if amax in (0.5234375, 0.5390625):
+        assert np.float32(qs_ref) != np.float32(O.quant_tensor(x, fmt)[2])
 
 
 def test_determinism(dev):

@@ -216,6 +216,35 @@ def test_scale_formulas_distinguish_block_channel_tensor():
     assert ds == f32(1.0) / qs
 
 
+@pytest.mark.parametrize("fmt", ["e4m3", "e5m2"])
+def test_torchao_tensorwise_form(fmt):
+    """scale_dt F64: torchao's amax_to_scale + cast (the reference layer's
+    modules/float8/float8_utils.py:45-48, :134-137 and
+    float8_training_tensor.py:153-154) evaluated by torch's own CPU ops: the
+    fp64 division, its rounding to fp32 and torch's fp8 cast. The amax is one
+    where fp32(448 / fp64(amax)) differs from the fp32 form (1 / amax) * 448,
+    so dropping the fp64 step fails; a tiny tensor takes the eps floor."""
+    f8 = {"e4m3": torch.float8_e4m3fn, "e5m2": torch.float8_e5m2}[fmt]
+    fmax = torch.finfo(f8).max
+    g = torch.Generator().manual_seed(11)
+    for amax_v in (0.5234375, 3.0e-13, 0.0):
+        x = (torch.rand(3, 40, 72, generator=g) * 2 - 1) * 0.5
+        if amax_v < 1e-3:
+            x = x * amax_v
+        x = x.bfloat16()
+        x[1, 7, 5] = -amax_v
+        amax = x.abs().max()
+        s = (fmax / torch.clamp(amax.to(torch.float64), min=1e-12)).to(torch.float32)
+        q_ref = (x.to(torch.float32) * s).clamp(-fmax, fmax).to(f8).view(torch.uint8).numpy()
+        q, ds, qs = O.quant_tensor(x, fmt, scale_dt=O.F64)
+        assert np.float32(qs) == np.float32(s.item()), amax_v
+        assert np.float32(ds) == np.float32(s.reciprocal().item())
+        assert np.array_equal(q, q_ref)
+        if amax_v == 0.5234375:
+            _, _, qs32 = O.quant_tensor(x, fmt)
+            assert qs32 != qs
+
+
 def test_block_structure_brute_force():
     """Tiny ragged / 3-D / strided inputs: per-block amax found by a Python
     loop over the block's elements, scale by the closed form, bytes by the
