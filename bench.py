@@ -1037,8 +1037,8 @@ def published_bmm(torch, dev, steps, warmup, eager):
 def fused_probe(torch, dev, steps, warmup):
     """pcamd_bmm_quant_a (A quantized 1x128 inside the GEMM's K loop) next to
     its unfused equal (hip_per_block_quant, then hip_per_block_bmm), graph-
-    timed on the same inputs: bf16 A [M, K], e4m3 B [K, N] (N-major,
-    128x128 scales), bf16 C. The fused kernel quantizes each A row block once
+    timed on the same inputs: bf16 A [M, K] (two tensors in turn), e4m3 B
+    [K, N] (N-major, 128x128 scales), bf16 C. The fused kernel quantizes each A row block once
     per N tile, so it wins where few N tiles share A (small N) and loses as N
     grows; `default_path` names what hip_per_block_bmm_quant_a runs without
     always_fused (the fused kernel up to FUSED_MAX_N columns)."""
@@ -1046,17 +1046,19 @@ def fused_probe(torch, dev, steps, warmup):
                                                        hip_per_block_bmm_quant_a, hip_per_block_quant)
     g = torch.Generator(device=dev).manual_seed(0)
     rows = []
-    for m, k, n in [(32768, 4096, 128), (32768, 4096, 256), (16384, 4096, 512), (8192, 4096, 1024),
-                    (8192, 4096, 4096), (8192, 4096, 14336)]:
-        x = torch.randn(1, m, k, generator=g, device=dev).bfloat16()
+    for idx, (m, k, n) in enumerate([(32768, 4096, 128), (32768, 4096, 256), (16384, 4096, 512),
+                                     (8192, 4096, 1024), (8192, 4096, 4096), (8192, 4096, 14336)]):
+        # two A inputs in turn (2 x 268 MB at M = 32768: beyond the 256 MB MALL)
+        xs = [torch.randn(1, m, k, generator=g, device=dev).bfloat16() for _ in range(2)]
         qb = hip_per_block_quant((torch.randn(1, k, n, generator=g, device=dev) * 0.02).bfloat16(),
                                  block_m=128, block_n=128)
         out = torch.empty(1, m, n, device=dev, dtype=torch.bfloat16)
-        fused_ms, _ = graph_time(torch, lambda i: hip_per_block_bmm_quant_a(x, qb, out=out, always_fused=True),
-                                 steps, warmup)
+        fused = lambda i: hip_per_block_bmm_quant_a(xs[i % 2], qb, out=out, always_fused=True)  # noqa: E731
+        # the clocks settle under load before the first timing of the process
+        fused_ms, _ = graph_time(torch, fused, steps, warmup, settle_ms=SETTLE_MS if idx == 0 else 0.0)
 
         def unfused(i):
-            hip_per_block_bmm(hip_per_block_quant(x, block_m=1, block_n=128), qb, out=out)
+            hip_per_block_bmm(hip_per_block_quant(xs[i % 2], block_m=1, block_n=128), qb, out=out)
 
         unfused_ms, _ = graph_time(torch, unfused, steps, warmup)
         rows.append({"m": m, "k": k, "n": n, "fused_us": round(fused_ms * 1e3, 1),
@@ -1064,7 +1066,7 @@ def fused_probe(torch, dev, steps, warmup):
                      "fused_speedup": round(unfused_ms / fused_ms, 3),
                      "default_path": "fused" if n <= FUSED_MAX_N else "quantize_then_multiply"})
         print(rows[-1], file=sys.stderr, flush=True)
-        del x, qb, out
+        del xs, qb, out
         torch.cuda.empty_cache()
     print(json.dumps({"fused_quant_bmm": rows}))
 
