@@ -95,6 +95,17 @@ def test_quant_outliers_saturate_and_range(dev):
     assert q.float().abs().max().item() <= 448.0
 
 
+def test_fp16_all_zero_edge(dev):
+    # eps rounds to 0 in fp16: quant factor inf, reciprocal 0 as in the
+    # reference (kernels/fp8_bmm/fp8_warper.py:21-25); the elements are 0 * inf = NaN before
+    # the clamp, which here gives -448 (the reference leaves NaN to tl.clamp)
+    q, recip = fp8_quant(torch.zeros(4, 64, dtype=torch.float16, device=dev))
+    torch.cuda.synchronize()
+    assert recip.item() == 0.0
+    assert torch.equal(q.view(torch.uint8).unique().cpu(), torch.tensor([0xFE], dtype=torch.uint8))
+    assert torch.all((q.float() * recip.float()) == 0)
+
+
 def test_quant_zeros_and_roundtrip(dev):
     q, recip = _check_quant(torch.zeros(32, 64), dev)
     assert q.float().abs().max().item() == 0.0 and torch.isfinite(recip).item()
