@@ -970,7 +970,18 @@ __global__ __launch_bounds__(NT) void quant_dual_kernel(DualArgs a) {
   __shared__ __attribute__((aligned(16))) uint32_t tt[TCOL ? 128 * 32 : 1];
   const int t = threadIdx.x;
   const int lc = t & 15, rs = t >> 4;
-  const int64_t b = blockIdx.z, g = blockIdx.y, strip = blockIdx.x;
+  // XCD-aware block order. Workgroups go to the 8 XCDs in turn (linear id
+  // % 8); remapped, XCD x takes the x-th eighth of the blocks in
+  // strip-fastest order, so all strips of a row group run on one XCD and the
+  // row scales of its rows (one float per row and strip, a row pitch of
+  // n / 128 floats apart) fill their cache lines in one L2 instead of
+  // reaching HBM as partial lines from eight. A bijection on the grid.
+  const uint64_t gx = gridDim.x, gy = gridDim.y;
+  const uint64_t total = gx * gy * gridDim.z, per = total / 8;
+  const uint64_t lin = (uint64_t(blockIdx.z) * gy + blockIdx.y) * gx + blockIdx.x;
+  const uint64_t blk = lin < per * 8 ? (lin % 8) * per + lin / 8 : lin;
+  const int64_t strip = static_cast<int64_t>(blk % gx), g = static_cast<int64_t>((blk / gx) % gy),
+                b = static_cast<int64_t>(blk / (gx * gy));
   const int64_t col = strip * 128 + lc * 8;
   const int64_t r0 = g * 128;
   auto row_of = [&](int p) -> int64_t { return TCOL ? r0 + 4 * rs + p : r0 + p * RPP + rs; };
