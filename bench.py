@@ -835,12 +835,23 @@ def mem_ceiling(torch, dev, steps, warmup):
     like the workloads over rotating buffers beyond the 256 MB MALL:
     - 2:1 (the quantizers): bf16 -> fp8 conversion of [18432, 7168] (config 2's shape);
     - 1:1 (the dual quantizer): bf16 copy of [8192, 14336] (config 5's dY);
-    - 0:1 (config 4's output, 268 MB of its 311 MB): bf16 fill of [128, 2048, 512]."""
+    - 0:1 (config 4's output, 268 MB of its 311 MB): bf16 fill of [128, 2048, 512];
+    and the 1:1 mix once more with this library's own streaming copy
+    (pcamd_selftest_copy16: one 16-byte non-temporal load and store per lane)
+    at the shapes of config 5's dY and X."""
+    from practice_cuda_amd import _lib as L
+
+    def hip_copy(src, dst):
+        L.check(L.lib().pcamd_selftest_copy16(L.ptr(src), L.ptr(dst), src.numel() * src.element_size(),
+                                              L.stream_of(src)), "pcamd_selftest_copy16")
+
     res = {}
     cases = {
         "convert_bf16_to_fp8_18432x7168": ((18432, 7168), lambda src, dst: dst.copy_(src), torch.float8_e4m3fn, 3),
         "copy_bf16_8192x14336": ((8192, 14336), lambda src, dst: dst.copy_(src), torch.bfloat16, 4),
         "fill_bf16_128x2048x512": ((128, 2048, 512), lambda src, dst: dst.zero_(), torch.bfloat16, 2),
+        "hip_copy_bf16_8192x14336": ((8192, 14336), hip_copy, torch.bfloat16, 4),
+        "hip_copy_bf16_8192x4096": ((8192, 4096), hip_copy, torch.bfloat16, 4),
     }
     for name, (shape, op, odt, bpe) in cases.items():
         nsets = 4
@@ -853,7 +864,6 @@ def mem_ceiling(torch, dev, steps, warmup):
         del srcs, dsts
         torch.cuda.empty_cache()
     # per-launch floor: the 1x128 quantizer on one row, back to back in a graph
-    from practice_cuda_amd import _lib as L
     tiny = torch.randn(1, 7168, device=dev).bfloat16()
     ty = torch.empty(1, 7168, dtype=torch.float8_e4m3fn, device=dev)
     ts = torch.empty(1, 56, device=dev)

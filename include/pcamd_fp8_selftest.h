@@ -1,10 +1,13 @@
 /*
- * pcamd_fp8_selftest.h - test-only entry point of libpcamd_fp8.so.
+ * pcamd_fp8_selftest.h - test and measurement entry points of
+ * libpcamd_fp8.so.
  *
  * Not part of the product interface (include/pcamd_fp8.h): the test suite
- * calls it to pin the hardware fp8 conversion the quantizers use. It has no
- * counterpart in the reference (xuOAO/practice_cuda), whose fp8 casts are
- * Triton's `.to(fp8)` (fp8_training/fp8_bench/kernels/quant/per_block.py:47).
+ * calls them to pin the hardware fp8 conversion the quantizers use, and
+ * bench.py to measure the plain-copy ceiling the quantizers are compared
+ * with. They have no counterpart in the reference (xuOAO/practice_cuda),
+ * whose fp8 casts are Triton's `.to(fp8)`
+ * (fp8_training/fp8_bench/kernels/quant/per_block.py:47).
  */
 #ifndef PCAMD_FP8_SELFTEST_H
 #define PCAMD_FP8_SELFTEST_H
@@ -24,6 +27,15 @@ extern "C" {
  * PCAMD_E5M2 (4). Returns 0 or a negative status (see pcamd_fp8.h).
  */
 int pcamd_selftest_fp8_convert(int fmt, uint32_t *result, void *stream);
+
+/*
+ * Plain device copy y[i] = x[i] of `bytes` bytes (a multiple of 16, both
+ * pointers 16-byte aligned) in the quantizers' streaming layout: one 16-byte
+ * non-temporal load and store per lane, 256-thread workgroups. The 1 : 1
+ * read/write ceiling the dual quantizer is measured against. Returns 0 or a
+ * negative status.
+ */
+int pcamd_selftest_copy16(const void *x, void *y, int64_t bytes, void *stream);
 
 #ifdef __cplusplus
 }

@@ -1721,6 +1721,27 @@ extern "C" int pcamd_quant_tensor(const void* x, int x_dtype, int64_t batch, int
   return dispatch_dt_fmt<LaunchTensor>(x_dtype, y_dtype, a, flat, static_cast<hipStream_t>(stream));
 }
 
+// plain 16-byte-per-lane streaming copy (measurement of the 1 : 1 ceiling)
+__global__ __launch_bounds__(kGroupThreads) void copy16_kernel(const u32x4_t* __restrict__ x,
+                                                             u32x4_t* __restrict__ y, int64_t chunks) {
+  const int64_t ch = int64_t(blockIdx.x) * kGroupThreads + threadIdx.x;
+  if (ch < chunks) __builtin_nontemporal_store(__builtin_nontemporal_load(x + ch), y + ch);
+}
+
+extern "C" int pcamd_selftest_copy16(const void* x, void* y, int64_t bytes, void* stream) {
+  clear_error();
+  if (bytes < 0 || bytes % 16) return set_error(PCAMD_ERR_INVALID, "bytes must be a non-negative multiple of 16");
+  if (bytes == 0) return PCAMD_OK;
+  if (!x || !y) return set_error(PCAMD_ERR_INVALID, "null pointer");
+  if ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(y)) & 15)
+    return set_error(PCAMD_ERR_INVALID, "pointers must be 16-byte aligned");
+  const int64_t chunks = bytes / 16, grid = (chunks + kGroupThreads - 1) / kGroupThreads;
+  if (grid > INT32_MAX) return set_error(PCAMD_ERR_UNSUPPORTED, "copy too large");
+  copy16_kernel<<<static_cast<uint32_t>(grid), kGroupThreads, 0, static_cast<hipStream_t>(stream)>>>(
+      static_cast<const u32x4_t*>(x), static_cast<u32x4_t*>(y), chunks);
+  return check_launch("copy16_kernel");
+}
+
 extern "C" int pcamd_selftest_fp8_convert(int fmt, uint32_t* result, void* stream) {
   clear_error();
   if (!result) return set_error(PCAMD_ERR_INVALID, "null result pointer");

@@ -40,6 +40,11 @@ def test_test_only_symbols_live_in_their_own_header():
         assert hasattr(L, name)
     assert L.pcamd_selftest_fp8_convert(7, FAKE, None) == -1
     assert b"fp8 format" in L.pcamd_last_error()
+    assert L.pcamd_selftest_copy16(FAKE, FAKE, 24, None) == -1
+    assert b"multiple of 16" in L.pcamd_last_error()
+    assert L.pcamd_selftest_copy16(ctypes.c_void_p(0x10008), FAKE, 32, None) == -1
+    assert b"aligned" in L.pcamd_last_error()
+    assert L.pcamd_selftest_copy16(FAKE, FAKE, 0, None) == 0
 
 
 def test_abi_version_matches_header():

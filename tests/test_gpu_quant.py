@@ -63,6 +63,16 @@ def make_input(shape, dtype, seed, scale=1.0, outliers=0.0):
 # ---------------------------------------------------------------------------
 # hardware fp8 conversion == integer restatement over every in-range fp32
 # ---------------------------------------------------------------------------
+@pytest.mark.parametrize("nbytes", [16, 4096 * 16 + 48, 8192 * 4096 * 2])
+def test_copy16_selftest(dev, nbytes):
+    # the plain copy that bench.py --mem-ceiling times as the 1:1 ceiling
+    x = torch.randint(0, 256, (nbytes,), dtype=torch.uint8, device=dev)
+    y = torch.zeros_like(x)
+    _lib.check(_lib.lib().pcamd_selftest_copy16(_lib.ptr(x), _lib.ptr(y), nbytes, _lib.stream_of(x)), "copy16")
+    torch.cuda.synchronize()
+    assert torch.equal(x, y)
+
+
 @pytest.mark.parametrize("fmt", [_lib.E4M3FN, _lib.E5M2])
 def test_hw_convert_selftest(dev, fmt):
     res = torch.zeros(4, dtype=torch.int32, device=dev)
