@@ -1,7 +1,8 @@
 """Seeded random shapes through every quantizer entry point, bit-exact against
 the oracle: ragged and aligned sizes, batches, all three input dtypes, both
 fp8 formats, power-of-two blocks, both channel axes, per-tensor, and the dual
-quantizer with either 128x1 layout. Each case prints its parameters first."""
+quantizer with either 128x1 layout; then the registered BMMs and the fused
+activation-quant BMM at the BMM bar. Each case prints its parameters first."""
 from __future__ import annotations
 
 import numpy as np
@@ -104,3 +105,49 @@ def test_random_bmm_case(dev, i):
     assert out.shape == (c["b"], c["m"], c["n"])
     err = O.max_abs_rel(out.float().cpu().numpy(), ref)
     assert err <= TOL, f"max_abs_rel {err}"
+
+
+def _fused_case(i):
+    rng = np.random.default_rng(3000 + i)
+    return {
+        "b": int(rng.choice([1, 1, 2, 3])),
+        "m": int(rng.choice([1, 17, 128, 129, 300, 1000])),
+        "n": int(rng.choice([16, 48, 64, 96, 128, 144, 192, 240, 256, 272, 384])),
+        "k": int(rng.choice([128, 256, 384, 512, 768, 1024, 1536, 2048])),
+        "dtype": str(rng.choice(["bf16", "f16"])),
+        "fmt": str(rng.choice(["e4m3", "e5m2"])),
+        "qbn": int(rng.choice([128, 128, 256, 32, 1])),
+        "b_k": bool(rng.integers(2)),
+        "wq": bool(rng.integers(2)),
+        "always": bool(rng.integers(2)),
+    }
+
+
+@pytest.mark.parametrize("i", range(24))
+def test_random_fused_quant_bmm_case(dev, i):
+    """Seeded random shapes through hip_per_block_bmm_quant_a, in and around
+    the streaming kernel's envelope (N <= 256, K % 256 == 0, quant-N blocks
+    >= 128): the quantized A is the 1 x 128 quantizer's bit for bit, the
+    product equals quantize-then-multiply to fp32 rounding and is within
+    max-abs-rel 1e-2 of the fp64 product of the dequantized operands."""
+    from practice_cuda_amd.impls.hip_per_block import hip_per_block_bmm, hip_per_block_bmm_quant_a
+    c = _fused_case(i)
+    print(f"fused quant bmm fuzz {i}: {c}", flush=True)
+    g = torch.Generator().manual_seed(4000 + i)
+    x = (torch.randn(c["b"], c["m"], c["k"], generator=g) * 2).to(DT[c["dtype"]]).to(dev)
+    w = torch.randn(c["b"], c["k"], c["n"], generator=g) * 0.05
+    if c["b_k"]:
+        w = w.transpose(-1, -2).contiguous().transpose(-1, -2)
+    qb = hip_per_block_quant(w.bfloat16().to(dev), block_m=128, block_n=c["qbn"], fp8_dtype=FMT[c["fmt"]])
+    res = hip_per_block_bmm_quant_a(x, qb, return_quant=c["wq"], always_fused=c["always"])
+    out, qa = res if c["wq"] else (res, None)
+    ref_q = hip_per_block_quant(x, block_m=1, block_n=128, fp8_dtype=FMT[c["fmt"]])
+    unfused = hip_per_block_bmm(ref_q, qb)
+    torch.cuda.synchronize()
+    if qa is not None:
+        assert torch.equal(qa.tensor.view(torch.uint8), ref_q.tensor.view(torch.uint8))
+        assert torch.equal(qa.dequant_scale.view(torch.int32), ref_q.dequant_scale.view(torch.int32))
+    scale = unfused.float().abs().max().item()
+    assert (out.float() - unfused.float()).abs().max().item() <= 1e-6 * scale + 1e-30
+    ref = O.bmm_reference(ref_q.dequantize().double().cpu().numpy(), qb.dequantize().double().cpu().numpy())
+    assert O.max_abs_rel(out.float().cpu().numpy(), ref) <= 1e-2
