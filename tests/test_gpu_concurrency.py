@@ -17,7 +17,8 @@ import pytest
 import torch
 
 from practice_cuda_amd import _lib
-from practice_cuda_amd.impls.hip_per_block import hip_per_block_bmm, hip_per_block_quant, hip_per_block_quant_dual
+from practice_cuda_amd.impls.hip_per_block import (hip_per_block_bmm, hip_per_block_bmm_quant_a, hip_per_block_quant,
+                                                   hip_per_block_quant_dual)
 from practice_cuda_amd.impls.hip_per_channel import hip_per_channel_quant
 from practice_cuda_amd.registry import QuantResult
 
@@ -37,7 +38,9 @@ def _inputs(dev, seed):
 
 def _run(x, w, a4, b4):
     """Quantizers (row groups, per-row channel, 128x128 tiles, the dual
-    kernel), the wide BMM (K = 1024) and the streaming BMM (K = 128, N = 512)."""
+    kernel), the wide BMM (K = 1024), the streaming BMM (K = 128, N = 512)
+    and the fused activation-quant BMM (N = 128, K = 1024: its streaming
+    kernel)."""
     qx = hip_per_block_quant(x[None], block_m=1, block_n=128)
     qw = hip_per_block_quant(w[None], block_m=128, block_n=128)
     qc = hip_per_channel_quant(x, channel_axis=-2)
@@ -48,8 +51,13 @@ def _run(x, w, a4, b4):
     qa4 = hip_per_block_quant(a4, block_m=1, block_n=128)
     qb4 = hip_per_block_quant(b4, block_m=128, block_n=128)
     y4 = hip_per_block_bmm(qa4, qb4)
+    qw128 = hip_per_block_quant(w[None, :128], block_m=128, block_n=128)
+    wt128 = QuantResult(qw128.tensor.transpose(-1, -2), qw128.dequant_scale.transpose(-1, -2), qw128.impl,
+                        "block", {"block_m": 128, "block_n": 128})
+    y5, qa5 = hip_per_block_bmm_quant_a(x[None], wt128, return_quant=True)
     return [qx.tensor, qx.dequant_scale, qw.tensor, qw.dequant_scale, qc.tensor, qc.dequant_scale,
-            r_row.tensor, r_row.dequant_scale, r_col.tensor.contiguous(), r_col.dequant_scale, y, y4]
+            r_row.tensor, r_row.dequant_scale, r_col.tensor.contiguous(), r_col.dequant_scale, y, y4,
+            y5, qa5.tensor, qa5.dequant_scale]
 
 
 def _bits(t):
