@@ -7,8 +7,8 @@ from __future__ import annotations
 import pytest
 import torch
 
-from practice_cuda_amd.impls.hip_per_block import (hip_per_block_bmm, hip_per_block_quant,
-                                                   hip_per_block_quant_dual)
+from practice_cuda_amd.impls.hip_per_block import (hip_per_block_bmm, hip_per_block_bmm_quant_a,
+                                                   hip_per_block_quant, hip_per_block_quant_dual)
 from practice_cuda_amd.impls.hip_per_channel import hip_per_channel_quant
 from practice_cuda_amd.impls.hip_per_tensor import hip_per_tensor_quant
 
@@ -90,9 +90,16 @@ def test_bmm_replay(dev):
     b2 = torch.randn(1, 256, 47, generator=g).bfloat16().to(dev)
     qa2 = hip_per_block_quant(a2, block_m=1, block_n=128)
     qb2 = hip_per_block_quant(b2, block_m=128, block_n=128)
+    b3 = torch.randn(2, 512, 128, generator=g).bfloat16().to(dev)  # N = 128: fused streaming kernel
+    b4 = torch.randn(2, 512, 256, generator=g).bfloat16().to(dev)  # N = 256
+    qb3 = hip_per_block_quant(b3, block_m=128, block_n=128)
+    qb4 = hip_per_block_quant(b4, block_m=128, block_n=128)
     fns = {
         "wide": lambda: hip_per_block_bmm(qa, qb),
         "single": lambda: hip_per_block_bmm(qa1, qb1),
         "general": lambda: hip_per_block_bmm(qa2, qb2),
+        "fused_stream_n128": lambda: hip_per_block_bmm_quant_a(ah, qb3, return_quant=True),
+        "fused_stream_n256": lambda: hip_per_block_bmm_quant_a(ah, qb4),
+        "fused_tiled": lambda: hip_per_block_bmm_quant_a(ah, qb, always_fused=True),
     }
     _replay_matches_eager(dev, fns)
