@@ -611,7 +611,7 @@ extern "C" int pcamd_bmm_scaled_mixed(const void* a, int a_dtype, const void* b,
 // groups along K, the quantizer's exact bytes and scales); see
 // include/pcamd_fp8.h. Layouts outside the fused kernel's envelope return
 // PCAMD_ERR_UNSUPPORTED so the caller can quantize and multiply separately.
-// PCAMD_BMM_FUSED_STREAM=0: narrow fused products take the 128 x 256 kernel too (read once)
+// PCAMD_BMM_FUSED_STREAM=0 (read once per process): narrow fused products take the 128 x 256 kernel too
 static bool fused_stream_disabled() {
   static const bool off = [] {
     const char* e = getenv("PCAMD_BMM_FUSED_STREAM");
