@@ -145,3 +145,40 @@ def test_repack_invalid_arguments(over, rc, msg):
 
 def test_repack_empty_is_ok():
     assert _repack(r=0) == 0 and _repack(c=0) == 0 and _repack(b=0) == 0
+
+
+def _bmm_quant_a(**over):
+    args = dict(a=FAKE, ad=_lib.BF16, b=FAKE, abd=_lib.E4M3FN, B=1, M=128, N=128, K=256,
+                sab=0, sam=256, sak=1, sbb=0, sbk=128, sbn=1, c=FAKE, cd=_lib.BF16, scb=0, scm=128, scn=1,
+                bias=None, biasd=0, sbb0=0, sbm=0, sbn0=0, sb=FAKE, ssbb=0, ssb1=1, ssb2=1, qbn=128,
+                qa=None, sqab=0, sqam=0, sqak=0, sa=None, soab=0, soam=0, soak=0,
+                fmax=448.0, eps=1e-12, act=0, st=None)
+    args.update(over)
+    return _lib.lib().pcamd_bmm_quant_a(*args.values())
+
+
+@pytest.mark.parametrize("over,rc,msg", [
+    (dict(ad=_lib.F32), -1, b"bf16"),
+    (dict(abd=_lib.BF16), -1, b"fp8"),
+    (dict(cd=9), -1, b"output dtype"),
+    (dict(bias=FAKE, biasd=_lib.E4M3FN), -1, b"bias dtype"),
+    (dict(M=-1), -1, b"negative size"),
+    (dict(act=3), -1, b"activation"),
+    (dict(fmax=0.0), -1, b"fp8_max"),
+    (dict(eps=-1.0), -1, b"eps"),
+    (dict(qbn=96), -1, b"power of two"),
+    (dict(qa=FAKE), -1, b"together"),
+    (dict(sb=None), -1, b"null"),
+    (dict(scn=2), -1, b"contiguous along N"),
+    # outside the fused envelope: the caller quantizes, then multiplies
+    (dict(K=200), -2, b"multiple of 128"),
+    (dict(sak=128, sam=1), -2, b"K-major"),
+])
+def test_bmm_quant_a_invalid_arguments(over, rc, msg):
+    assert _bmm_quant_a(**over) == rc
+    assert msg in _lib.lib().pcamd_last_error()
+
+
+def test_bmm_quant_a_empty_is_ok():
+    assert _bmm_quant_a(M=0) == 0 and _bmm_quant_a(N=0) == 0 and _bmm_quant_a(B=0) == 0
+    assert _lib.lib().pcamd_last_error() == b""
