@@ -1349,14 +1349,13 @@ struct LaunchDual {
   static int go(const DualArgs& a, int64_t batch, bool tcol, hipStream_t st) {
     const dim3 grid(static_cast<uint32_t>((a.n + 127) / 128), static_cast<uint32_t>((a.m + 127) / 128),
                     static_cast<uint32_t>(batch));
-    constexpr int NT = 512;  // 256: 3 % slower at [8192, 14336]; 1024: 4 % slower
     const bool full = a.m % 128 == 0 && a.n % 128 == 0;
     if (clamp_free<FMT>(a.fp8_max, a.eps)) return go2<NTS, false>(a, grid, full, tcol, st);
     return go2<NTS, true>(a, grid, full, tcol, st);
   }
   template <bool NTS, bool CLAMP>
   static int go2(const DualArgs& a, dim3 grid, bool full, bool tcol, hipStream_t st) {
-    constexpr int NT = 512;
+    constexpr int NT = 512;  // 256: 3 % slower at [8192, 14336]; 1024: 4 % slower
     if (tcol && full) quant_dual_kernel<DT, FMT, NT, NTS, true, true, CLAMP><<<grid, NT, 0, st>>>(a);
     else if (tcol) quant_dual_kernel<DT, FMT, NT, NTS, false, true, CLAMP><<<grid, NT, 0, st>>>(a);
     else if (full) quant_dual_kernel<DT, FMT, NT, NTS, true, false, CLAMP><<<grid, NT, 0, st>>>(a);
