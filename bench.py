@@ -1051,7 +1051,8 @@ def fused_probe(torch, dev, steps, warmup):
     [K, N] (N-major, 128x128 scales), bf16 C. The fused kernel quantizes each A row block once
     per N tile, so it wins where few N tiles share A (small N) and loses as N
     grows; `default_path` names what hip_per_block_bmm_quant_a runs without
-    always_fused (the fused kernel up to FUSED_MAX_N columns)."""
+    always_fused (the fused call inside the streaming kernel's envelope: here
+    up to FUSED_MAX_N columns, K = 4096)."""
     from practice_cuda_amd.impls.hip_per_block import (FUSED_MAX_N, hip_per_block_bmm,
                                                        hip_per_block_bmm_quant_a, hip_per_block_quant)
     g = torch.Generator(device=dev).manual_seed(0)

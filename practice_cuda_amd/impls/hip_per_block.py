@@ -218,6 +218,16 @@ def hip_per_block_bmm(
 FUSED_MAX_N = 256
 
 
+def _fused_streams(n: int, k: int, qbn: int, bias, activation: str, out_dtype) -> bool:
+    """Whether pcamd_bmm_quant_a runs its streaming kernel for this product
+    (one workgroup holds all N columns and reads A once): the envelope of
+    bmm_fused_stream_ok. Outside it the call runs the tiled fused kernel,
+    which quantizes A once per 256-column tile and is slower than quantizing
+    first at every measured shape."""
+    return (0 < n <= FUSED_MAX_N and n % 16 == 0 and k >= 256 and k % 256 == 0 and qbn >= 128
+            and bias is None and activation == "none" and out_dtype in (torch.bfloat16, torch.float16))
+
+
 def hip_per_block_bmm_quant_a(
     x: torch.Tensor,
     b: QuantResult,
@@ -243,11 +253,13 @@ def hip_per_block_bmm_quant_a(
     (kernels/fp8_bmm/kernel/fp8_quant_bmm_fused_kernel.py:30-146, unfinished
     there), on the per-block recipe. Layouts the fused kernel does not cover
     (an M-major or unaligned x, K not a multiple of 128) take the two-kernel
-    path: hip_per_block_quant, then hip_per_block_bmm. So do products wider
-    than FUSED_MAX_N columns unless always_fused is set: the fused kernel
-    quantizes each A row block once per 256-column tile of C, and from two
-    tiles on the two-kernel path is faster (MI355X, M 16384, K 4096, N 512:
-    133 vs 93 us)."""
+    path: hip_per_block_quant, then hip_per_block_bmm. Unless always_fused is
+    set, so do the products outside the streaming kernel's envelope (N up to
+    FUSED_MAX_N and a multiple of 16, K a multiple of 256, B's quant-N blocks
+    >= 128, no bias or activation, bf16/fp16 output): there the fused call
+    runs a tiled kernel that quantizes each A row block once per 256-column
+    tile of C, and the two-kernel path is faster (MI355X, A [32768, 4096],
+    N 128: 134.7 vs 125.2 us; M 16384, N 512: 133 vs 93 us)."""
     if x.ndim not in (2, 3):
         raise ValueError(f"fused quant BMM expects a 2D or 3D activation, got {tuple(x.shape)}")
     if x.dtype not in (torch.bfloat16, torch.float16):
@@ -279,7 +291,8 @@ def hip_per_block_bmm_quant_a(
         sa = torch.empty((batch, m, -(-k // 128)), device=x3.device, dtype=torch.float32)
     L = _lib.lib()
     rc = _lib.ERR_UNSUPPORTED
-    if in_b in ("n-major", "k-major") and x3.stride(-1) == 1 and (always_fused or n <= FUSED_MAX_N):
+    fused = always_fused or _fused_streams(n, k, qbn, bias, activation, out.dtype)
+    if in_b in ("n-major", "k-major") and x3.stride(-1) == 1 and fused:
         with torch.cuda.device(x3.device):
             rc = L.pcamd_bmm_quant_a(
                 _lib.ptr(x3), _lib.dtype_code(x3.dtype), _lib.ptr(b.tensor), _lib.dtype_code(fp8_dtype),

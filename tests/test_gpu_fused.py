@@ -105,7 +105,8 @@ def test_fused_bias_activation_out_dtype(dev, activation):
     x = _rand((2, 160, 256), 3).to(dev)
     qb = _b_operand(2, 256, 192, 4, dev)
     bias = _rand((2, 160, 192), 5).to(dev)
-    out = hip_per_block_bmm_quant_a(x, qb, bias=bias, activation=activation, out_dtype=torch.float32)
+    out = hip_per_block_bmm_quant_a(x, qb, bias=bias, activation=activation, out_dtype=torch.float32,
+                                    always_fused=True)
     qa = hip_per_block_quant(x, block_m=1, block_n=128)
     ref = hip_per_block_bmm(qa, qb, bias=bias, activation=activation, out_dtype=torch.float32)
     torch.cuda.synchronize()
@@ -147,10 +148,27 @@ def test_wide_products_take_two_kernel_path(dev):
     assert (fused.float() - ref.float()).abs().max().item() <= 1e-6 * ref.float().abs().max().item()
 
 
+@pytest.mark.parametrize("k,n,qbn,extra", [(384, 128, 128, {}), (512, 128, 32, {}),
+                                           (512, 128, 128, {"activation": "gelu"}),
+                                           (512, 120, 128, {}), (512, 128, 128, {"out_dtype": torch.float32})])
+def test_narrow_products_outside_the_stream_envelope_take_two_kernels(dev, k, n, qbn, extra):
+    # N <= 256 but K % 256 != 0, quant-N blocks < 128, an activation, N % 16
+    # != 0 or an fp32 output: by default the unfused results exactly
+    print(f"fused default path k={k} n={n} qbn={qbn} {extra}", flush=True)
+    x = _rand((1, 200, k), 17).to(dev)
+    qb = _b_operand(1, k, n, 18, dev, qbn=qbn)
+    out, qa = hip_per_block_bmm_quant_a(x, qb, return_quant=True, **extra)
+    ref_q = hip_per_block_quant(x, block_m=1, block_n=128)
+    ref = hip_per_block_bmm(ref_q, qb, **extra)
+    torch.cuda.synchronize()
+    assert torch.equal(out, ref)
+    assert torch.equal(qa.tensor.view(torch.uint8), ref_q.tensor.view(torch.uint8))
+
+
 def test_fused_2d_activation(dev):
     x = _rand((256, 384), 8).to(dev)
     qb = _b_operand(1, 384, 256, 9, dev)
-    out = hip_per_block_bmm_quant_a(x, qb)
+    out = hip_per_block_bmm_quant_a(x, qb, always_fused=True)
     ref = hip_per_block_bmm(hip_per_block_quant(x[None], block_m=1, block_n=128), qb)[0]
     torch.cuda.synchronize()
     assert out.shape == (256, 256)
