@@ -236,9 +236,9 @@ int pcamd_bmm_scaled_mixed(const void *a, int a_dtype, const void *b,
  * contiguous along k, 8-byte aligned rows) receive the quantized A and its
  * scales [batch, m, k/128]. k must be a positive multiple of 128; other
  * layouts return PCAMD_ERR_UNSUPPORTED (quantize, then pcamd_bmm_scaled).
- * The call pays off for n <= 256 (with k a multiple of 256, quant-N blocks of
- * at least 128 and no bias or activation, one workgroup holds every column
- * and reads a once); wider products quantize each 128-row block of a once per
+ * The call pays off for n <= 256 (with n a multiple of 16, k a multiple of
+ * 256 and quant-N blocks of at least 128, one workgroup holds every column
+ * and reads a once; any bias, activation and output type); wider products quantize each 128-row block of a once per
  * 256-column tile of c, where quantizing first and then multiplying is
  * faster. Replaces the intent of the reference's fused quant + BMM kernel
  * (kernels/fp8_bmm/kernel/fp8_quant_bmm_fused_kernel.py:30-146), whose

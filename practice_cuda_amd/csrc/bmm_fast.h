@@ -52,7 +52,7 @@ int bmm_fused_launch(const FastArgs& a, int a_dtype, int fmt, bool b_k, bool sb_
 
 // the same product for narrow N (bmm_fused_stream.hip): A streamed once,
 // quantized in registers; bmm_fused_stream_ok is its envelope (N <= 256,
-// N % 16 == 0, K % 256 == 0, qbn >= 128, plain 16-bit output)
+// N % 16 == 0, K % 256 == 0, qbn >= 128, C contiguous along N)
 bool bmm_fused_stream_ok(const FastArgs& a, int64_t batch, int64_t qbn);
 int bmm_fused_stream_launch(const FastArgs& a, int a_dtype, int fmt, bool b_k, int64_t batch, hipStream_t st);
 

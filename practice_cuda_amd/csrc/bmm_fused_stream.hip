@@ -18,8 +18,8 @@
 //
 // Envelope (pcamd_bmm_quant_a checks it; other calls take the 128 x 256
 // fused kernel of bmm_fast.hip): N <= 256 and a multiple of 16, K a multiple
-// of 256, B's column blocks qbn >= 128, plain 16-bit output, no bias or
-// activation.
+// of 256, B's column blocks qbn >= 128, C contiguous along N; any bias,
+// activation and output type.
 #include <hip/hip_runtime.h>
 
 #include <cmath>
@@ -283,16 +283,53 @@ __global__ __launch_bounds__(NT, 1) void bmm_fused_stream_kernel(FastArgs a) {
     for (int r = 0; r < 4; ++r) acc[j][r] += p[j & 1][r] * pf[j & 1];
   }
 
-  // epilogue: row `row`, columns 16 j + 4 lg .. + 3 of each sub-tile
+  // epilogue: row `row`, columns 16 j + 4 lg .. + 3 of each sub-tile, in
+  // the reference's order: scaled product, + bias, activation, one rounding
+  // to C's type (kernels/bmm/per_block.py:113-137). A 16-bit C (and bias,
+  // if any) with 8-byte aligned rows takes 8-byte loads and stores; other
+  // types and strides go through the general epilogue.
   if (row < a.m) {
-    uint16_t* crow = reinterpret_cast<uint16_t*>(a.c) + bidx * a.scb + int64_t(row) * a.scm;
-    const bool f16 = a.c_dtype == kF16;
+    const bool c16 = (a.c_dtype == kBF16 || a.c_dtype == kF16) && a.scm % 4 == 0 && a.scb % 4 == 0 &&
+                     (reinterpret_cast<uintptr_t>(a.c) & 7) == 0;
+    const bool b16 = a.bias == nullptr || ((a.bias_dtype == kBF16 || a.bias_dtype == kF16) && a.sbiasn == 1 &&
+                                           a.sbiasm % 4 == 0 && a.sbiasb % 4 == 0 &&
+                                           (reinterpret_cast<uintptr_t>(a.bias) & 7) == 0);
+    if (c16 && b16) {
+      uint16_t* crow = reinterpret_cast<uint16_t*>(a.c) + bidx * a.scb + int64_t(row) * a.scm;
+      const uint16_t* brow =
+          a.bias ? static_cast<const uint16_t*>(a.bias) + bidx * a.sbiasb + int64_t(row) * a.sbiasm : nullptr;
+      const bool f16 = a.c_dtype == kF16, bias_bf16 = a.bias_dtype == kBF16, gelu = a.act == PCAMD_ACT_GELU;
 #pragma unroll
-    for (int j = 0; j < JN; ++j) {
-      const int col = 16 * j + 4 * lg;
-      if (col < a.n)
-        *reinterpret_cast<uint2*>(crow + col) = make_uint2(pack16_pair<OUT16_RUNTIME>(acc[j][0], acc[j][1], f16),
-                                                           pack16_pair<OUT16_RUNTIME>(acc[j][2], acc[j][3], f16));
+      for (int j = 0; j < JN; ++j) {
+        const int col = 16 * j + 4 * lg;
+        if (col < a.n) {
+          float v[4] = {acc[j][0], acc[j][1], acc[j][2], acc[j][3]};
+          if (brow) {
+            const uint2 h = *reinterpret_cast<const uint2*>(brow + col);
+            const uint32_t e[4] = {h.x & 0xFFFFu, h.x >> 16, h.y & 0xFFFFu, h.y >> 16};
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+              v[r] += bias_bf16 ? __uint_as_float(e[r] << 16)
+                                : static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(e[r])));
+          }
+          if (gelu) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) v[r] = 0.5f * v[r] * (1.0f + erff(v[r] * 0.7071067811865475f));
+          }
+          *reinterpret_cast<uint2*>(crow + col) = make_uint2(pack16_pair<OUT16_RUNTIME>(v[0], v[1], f16),
+                                                             pack16_pair<OUT16_RUNTIME>(v[2], v[3], f16));
+        }
+      }
+    } else {
+      const int64_t c_row = bidx * a.scb + int64_t(row) * a.scm;
+      const int64_t bias_row = bidx * a.sbiasb + int64_t(row) * a.sbiasm;
+#pragma unroll
+      for (int j = 0; j < JN; ++j) {
+        const int col = 16 * j + 4 * lg;
+        if (col < a.n)
+          bmmw::epilogue_general(a.c, c_row, a.c_dtype, a.bias, bias_row, a.sbiasn, a.bias_dtype, a.act, col,
+                                 min(4, a.n - col), acc[j][0], acc[j][1], acc[j][2], acc[j][3]);
+      }
     }
   }
 }
@@ -337,9 +374,7 @@ int launch_dt(const FastArgs& a, bool b_k, int64_t batch, hipStream_t st) {
 }  // namespace bmmq
 
 bool bmm_fused_stream_ok(const FastArgs& a, int64_t batch, int64_t qbn) {
-  return a.n > 0 && a.n <= 256 && a.n % 16 == 0 && a.k >= 256 && a.k % 256 == 0 && qbn >= 128 &&
-         a.bias == nullptr && a.act == PCAMD_ACT_NONE && (a.c_dtype == kBF16 || a.c_dtype == kF16) &&
-         a.scn == 1 && a.scm % 4 == 0 && a.scb % 4 == 0 && (reinterpret_cast<uintptr_t>(a.c) & 7) == 0 &&
+  return a.n > 0 && a.n <= 256 && a.n % 16 == 0 && a.k >= 256 && a.k % 256 == 0 && qbn >= 128 && a.scn == 1 &&
          batch <= 65535 && a.m <= INT32_MAX - bmmq::ROWS &&
          (!a.qa_out || (a.sqam % 8 == 0 && a.sqab % 8 == 0 && (reinterpret_cast<uintptr_t>(a.qa_out) & 7) == 0 &&
                         a.m * a.sqam + a.k < (int64_t{1} << 31) &&

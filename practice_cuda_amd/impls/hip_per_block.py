@@ -218,14 +218,14 @@ def hip_per_block_bmm(
 FUSED_MAX_N = 256
 
 
-def _fused_streams(n: int, k: int, qbn: int, bias, activation: str, out_dtype) -> bool:
+def _fused_streams(n: int, k: int, qbn: int) -> bool:
     """Whether pcamd_bmm_quant_a runs its streaming kernel for this product
     (one workgroup holds all N columns and reads A once): the envelope of
-    bmm_fused_stream_ok. Outside it the call runs the tiled fused kernel,
-    which quantizes A once per 256-column tile and is slower than quantizing
-    first at every measured shape."""
-    return (0 < n <= FUSED_MAX_N and n % 16 == 0 and k >= 256 and k % 256 == 0 and qbn >= 128
-            and bias is None and activation == "none" and out_dtype in (torch.bfloat16, torch.float16))
+    bmm_fused_stream_ok, for any bias, activation and output type. Outside it
+    the call runs the tiled fused kernel, which quantizes A once per
+    256-column tile and is slower than quantizing first at every measured
+    shape."""
+    return 0 < n <= FUSED_MAX_N and n % 16 == 0 and k >= 256 and k % 256 == 0 and qbn >= 128
 
 
 def hip_per_block_bmm_quant_a(
@@ -256,7 +256,7 @@ def hip_per_block_bmm_quant_a(
     path: hip_per_block_quant, then hip_per_block_bmm. Unless always_fused is
     set, so do the products outside the streaming kernel's envelope (N up to
     FUSED_MAX_N and a multiple of 16, K a multiple of 256, B's quant-N blocks
-    >= 128, no bias or activation, bf16/fp16 output): there the fused call
+    >= 128; bias, activation and output type are free): there the fused call
     runs a tiled kernel that quantizes each A row block once per 256-column
     tile of C, and the two-kernel path is faster (MI355X, A [32768, 4096],
     N 128: 134.7 vs 125.2 us; M 16384, N 512: 133 vs 93 us)."""
@@ -291,7 +291,7 @@ def hip_per_block_bmm_quant_a(
         sa = torch.empty((batch, m, -(-k // 128)), device=x3.device, dtype=torch.float32)
     L = _lib.lib()
     rc = _lib.ERR_UNSUPPORTED
-    fused = always_fused or _fused_streams(n, k, qbn, bias, activation, out.dtype)
+    fused = always_fused or _fused_streams(n, k, qbn)
     if in_b in ("n-major", "k-major") and x3.stride(-1) == 1 and fused:
         with torch.cuda.device(x3.device):
             rc = L.pcamd_bmm_quant_a(

@@ -100,18 +100,49 @@ def test_fused_clamped_instantiation(dev, n):
     assert (out.float() - unfused.float()).abs().max().item() <= 1e-6 * unfused.float().abs().max().item()
 
 
+@pytest.mark.parametrize("n,k", [(192, 256), (128, 512), (512, 256)])  # streaming (one / two K blocks), tiled
 @pytest.mark.parametrize("activation", ["none", "gelu"])
-def test_fused_bias_activation_out_dtype(dev, activation):
-    x = _rand((2, 160, 256), 3).to(dev)
-    qb = _b_operand(2, 256, 192, 4, dev)
-    bias = _rand((2, 160, 192), 5).to(dev)
-    out = hip_per_block_bmm_quant_a(x, qb, bias=bias, activation=activation, out_dtype=torch.float32,
-                                    always_fused=True)
+@pytest.mark.parametrize("out_dtype,bias_dtype", [(torch.float32, torch.bfloat16), (torch.bfloat16, torch.float32),
+                                                  (torch.float16, torch.float16), (torch.bfloat16, torch.bfloat16),
+                                                  (torch.float16, torch.bfloat16)])
+def test_fused_bias_activation_out_dtype(dev, n, k, activation, out_dtype, bias_dtype):
+    print(f"fused epilogue n={n} k={k} {activation} out={out_dtype} bias={bias_dtype}", flush=True)
+    x = _rand((2, 160, k), 3).to(dev)
+    qb = _b_operand(2, k, n, 4, dev)
+    bias = _rand((2, 160, n), 5).to(bias_dtype).to(dev)
+    out = hip_per_block_bmm_quant_a(x, qb, bias=bias, activation=activation, out_dtype=out_dtype)
+    forced = hip_per_block_bmm_quant_a(x, qb, bias=bias, activation=activation, out_dtype=out_dtype,
+                                       always_fused=True)
     qa = hip_per_block_quant(x, block_m=1, block_n=128)
-    ref = hip_per_block_bmm(qa, qb, bias=bias, activation=activation, out_dtype=torch.float32)
+    ref = hip_per_block_bmm(qa, qb, bias=bias, activation=activation, out_dtype=out_dtype)
     torch.cuda.synchronize()
-    assert out.dtype == torch.float32
-    assert (out - ref).abs().max().item() <= 1e-6 * ref.abs().max().item()
+    assert out.dtype == out_dtype and forced.dtype == out_dtype
+    # fp32 results to rounding; 16-bit ones to one unit in the last place
+    tol = 1e-6 if out_dtype == torch.float32 else 8e-3
+    for r in (out, forced):
+        assert (r.float() - ref.float()).abs().max().item() <= tol * ref.float().abs().max().item()
+
+
+@pytest.mark.parametrize("bias_layout", ["broadcast", "row_stride_2_mod_4", "odd_offset"])
+def test_fused_bias_layouts(dev, bias_layout):
+    """A 16-bit bias broadcast over batch and rows (strides 0) takes the
+    packed 8-byte epilogue; one whose rows are not 8-byte aligned takes the
+    per-element one. Both give the unfused product's results."""
+    print(f"fused bias layout {bias_layout}", flush=True)
+    n, k = 192, 256
+    x = _rand((2, 96, k), 21).to(dev)
+    qb = _b_operand(2, k, n, 22, dev)
+    if bias_layout == "broadcast":
+        bias = _rand((n,), 23).to(torch.bfloat16).to(dev).expand(2, 96, n)
+    elif bias_layout == "row_stride_2_mod_4":
+        bias = _rand((2, 96, n + 2), 23).to(torch.bfloat16).to(dev)[..., :n]
+    else:
+        bias = _rand((2 * 96 * n + 1,), 23).to(torch.bfloat16).to(dev)[1:].view(2, 96, n)
+    out = hip_per_block_bmm_quant_a(x, qb, bias=bias, activation="gelu", always_fused=True)
+    qa = hip_per_block_quant(x, block_m=1, block_n=128)
+    ref = hip_per_block_bmm(qa, qb, bias=bias, activation="gelu")
+    torch.cuda.synchronize()
+    assert (out.float() - ref.float()).abs().max().item() <= 8e-3 * ref.float().abs().max().item()
 
 
 @pytest.mark.parametrize("layout", ["m_major", "unaligned_k"])
@@ -149,11 +180,11 @@ def test_wide_products_take_two_kernel_path(dev):
 
 
 @pytest.mark.parametrize("k,n,qbn,extra", [(384, 128, 128, {}), (512, 128, 32, {}),
-                                           (512, 128, 128, {"activation": "gelu"}),
-                                           (512, 120, 128, {}), (512, 128, 128, {"out_dtype": torch.float32})])
+                                           (384, 128, 128, {"activation": "gelu"}),
+                                           (512, 120, 128, {}), (384, 256, 128, {"out_dtype": torch.float32})])
 def test_narrow_products_outside_the_stream_envelope_take_two_kernels(dev, k, n, qbn, extra):
-    # N <= 256 but K % 256 != 0, quant-N blocks < 128, an activation, N % 16
-    # != 0 or an fp32 output: by default the unfused results exactly
+    # N <= 256 but K % 256 != 0, quant-N blocks < 128 or N % 16 != 0: by
+    # default the unfused results exactly
     print(f"fused default path k={k} n={n} qbn={qbn} {extra}", flush=True)
     x = _rand((1, 200, k), 17).to(dev)
     qb = _b_operand(1, k, n, 18, dev, qbn=qbn)
