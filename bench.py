@@ -1052,8 +1052,9 @@ def fused_probe(torch, dev, steps, warmup):
     per N tile, so it wins where few N tiles share A (small N) and loses as N
     grows; `default_path` names what hip_per_block_bmm_quant_a runs without
     always_fused (the fused call inside the streaming kernel's envelope: here
-    up to FUSED_MAX_N columns, K = 4096)."""
-    from practice_cuda_amd.impls.hip_per_block import (FUSED_MAX_N, hip_per_block_bmm,
+    up to FUSED_MAX_N columns, K = 4096). Inside that envelope both paths are
+    timed again with a bf16 bias [M, N] and GELU in the epilogue."""
+    from practice_cuda_amd.impls.hip_per_block import (_fused_streams, hip_per_block_bmm,
                                                        hip_per_block_bmm_quant_a, hip_per_block_quant)
     g = torch.Generator(device=dev).manual_seed(0)
     rows = []
@@ -1072,10 +1073,25 @@ def fused_probe(torch, dev, steps, warmup):
             hip_per_block_bmm(hip_per_block_quant(xs[i % 2], block_m=1, block_n=128), qb, out=out)
 
         unfused_ms, _ = graph_time(torch, unfused, steps, warmup)
+        streams = _fused_streams(n, k, 128)
         rows.append({"m": m, "k": k, "n": n, "fused_us": round(fused_ms * 1e3, 1),
                      "quantize_then_multiply_us": round(unfused_ms * 1e3, 1),
                      "fused_speedup": round(unfused_ms / fused_ms, 3),
-                     "default_path": "fused" if n <= FUSED_MAX_N else "quantize_then_multiply"})
+                     "default_path": "fused" if streams else "quantize_then_multiply"})
+        if streams:
+            bias = torch.randn(1, m, n, generator=g, device=dev).bfloat16()
+
+            def fused_bg(i):
+                hip_per_block_bmm_quant_a(xs[i % 2], qb, out=out, bias=bias, activation="gelu", always_fused=True)
+
+            def unfused_bg(i):
+                hip_per_block_bmm(hip_per_block_quant(xs[i % 2], block_m=1, block_n=128), qb, out=out, bias=bias,
+                                  activation="gelu")
+
+            rows[-1]["fused_bias_gelu_us"] = round(graph_time(torch, fused_bg, steps, warmup)[0] * 1e3, 1)
+            rows[-1]["quantize_then_multiply_bias_gelu_us"] = round(
+                graph_time(torch, unfused_bg, steps, warmup)[0] * 1e3, 1)
+            del bias
         print(rows[-1], file=sys.stderr, flush=True)
         del xs, qb, out
         torch.cuda.empty_cache()

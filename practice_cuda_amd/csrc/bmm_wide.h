@@ -599,13 +599,12 @@ __global__ __launch_bounds__(NT, 1) void bmm_wide_kernel(FastArgs a) {
       return sam_v;
     };
     const bool plain = a.bias == nullptr && a.act == PCAMD_ACT_NONE && a.c_dtype == kBF16;
-    // the staged path also takes fp16 output and a 16-bit bias contiguous
-    // along N with 8-byte aligned rows (one load per lane's 4 columns);
-    // activations and other bias forms take the direct path below
+    // the staged path also takes fp16 output, GELU and a 16-bit bias
+    // contiguous along N with 8-byte aligned rows (one load per lane's 4
+    // columns); other bias forms and output types take the direct path below
     const bool bias16 = a.bias != nullptr && (a.bias_dtype == kBF16 || a.bias_dtype == kF16) && a.sbiasn == 1 &&
                         (a.sbiasm & 3) == 0 && (a.sbiasb & 3) == 0 && (reinterpret_cast<uintptr_t>(a.bias) & 7) == 0;
-    const bool out16 = (a.c_dtype == kBF16 || a.c_dtype == kF16) && a.act == PCAMD_ACT_NONE &&
-                       (a.bias == nullptr || bias16);
+    const bool out16 = (a.c_dtype == kBF16 || a.c_dtype == kF16) && (a.bias == nullptr || bias16);
     // (CT: the launcher checked the transposed output's alignment)
     if (CT || staged_output_ok(a.c, a.scb, a.scm, a.n, out16)) {
       // each wave stages its sub-tile in 8 KiB (4 KiB for a half tile) of the
@@ -646,11 +645,12 @@ __global__ __launch_bounds__(NT, 1) void bmm_wide_kernel(FastArgs a) {
           });
           return;
         }
-        // fp16 output and / or a 16-bit bias, in the reference's order: scaled
-        // product, + bias, one rounding (kernels/bmm/per_block.py:113-137). The
-        // output type is picked per element pair at run time (OUT16_RUNTIME),
-        // so this path is instantiated once.
-        const bool bias_bf16 = a.bias_dtype == kBF16;
+        // fp16 output, a 16-bit bias and / or GELU, in the reference's order:
+        // scaled product, + bias, activation, one rounding
+        // (kernels/bmm/per_block.py:113-137). The output type is picked per
+        // element pair at run time (OUT16_RUNTIME), so this path is
+        // instantiated once.
+        const bool bias_bf16 = a.bias_dtype == kBF16, gelu = a.act == PCAMD_ACT_GELU;
         const uint16_t* bias_b = bias16 ? static_cast<const uint16_t*>(a.bias) + bidx * a.sbiasb : nullptr;
         auto value = [&](int i, int j, float (&v)[4]) {
           float sbv[4];
@@ -665,6 +665,10 @@ __global__ __launch_bounds__(NT, 1) void bmm_wide_kernel(FastArgs a) {
             for (int r = 0; r < 4; ++r)
               v[r] += bias_bf16 ? __uint_as_float(e[r] << 16)
                                 : static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(e[r])));
+          }
+          if (gelu) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) v[r] = 0.5f * v[r] * (1.0f + erff(v[r] * 0.7071067811865475f));
           }
         };
         stage(IC<OUT16_RUNTIME>{}, value);

@@ -81,6 +81,40 @@ def test_bmm_bias_activation_dtypes(dev, out_dtype, activation):
     assert O.max_abs_rel(out.float().cpu().numpy(), ref) <= TOL
 
 
+@pytest.mark.parametrize("scheme", SCHEMES)
+@pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float16])
+def test_bmm_staged_gelu_matches_direct_epilogue(dev, scheme, out_dtype):
+    """A 16-bit bias with 8-byte aligned rows and GELU go through the staged
+    (LDS) epilogue; the same bias one element off alignment goes through the
+    per-element one. Same accumulators, same order of operations: with block
+    scales (applied in the K loop) the outputs are identical; with channel /
+    tensor scales the inlined path may contract scale and bias into one fma,
+    so they agree to one 16-bit unit. Partial tiles (M = 300, N = 136)."""
+    print(f"bmm staged gelu {scheme} {out_dtype}", flush=True)
+    impl = get_bmm(f"{scheme}_a_k_b_n")
+    quant = get_quant(impl.quant_impl)
+    qa = impl.prepare_a(quant.fn(rand((2, 300, 384), 12).to(dev), **impl.quant_a_kwargs))
+    qb = impl.prepare_b(quant.fn(rand((2, 384, 136), 13).to(dev), **impl.quant_b_kwargs))
+    kw = impl.prepare_call_kwargs(qa, qb)
+    bias = rand((2, 300, 136), 14).to(dev)
+    shifted = torch.empty(bias.numel() + 1, device=dev, dtype=bias.dtype)[1:].view_as(bias)
+    shifted.copy_(bias)
+    staged = impl.fn(qa, qb, bias=bias, activation="gelu", out_dtype=out_dtype, **kw)
+    direct = impl.fn(qa, qb, bias=shifted, activation="gelu", out_dtype=out_dtype, **kw)
+    no_bias = impl.fn(qa, qb, activation="gelu", out_dtype=out_dtype, **kw)
+    torch.cuda.synchronize()
+    if "per_block" in scheme:
+        assert torch.equal(staged, direct)
+    else:
+        assert (staged.float() - direct.float()).abs().max().item() <= 8e-3 * direct.float().abs().max().item()
+    ref = O.bmm_reference(qa.dequantize().double().cpu().numpy(), qb.dequantize().double().cpu().numpy(),
+                          bias.double().cpu().numpy(), "gelu")
+    assert O.max_abs_rel(staged.float().cpu().numpy(), ref) <= TOL
+    ref0 = O.bmm_reference(qa.dequantize().double().cpu().numpy(), qb.dequantize().double().cpu().numpy(),
+                           None, "gelu")
+    assert O.max_abs_rel(no_bias.float().cpu().numpy(), ref0) <= TOL
+
+
 def test_bmm_fp8_output_saturates(dev):
     # reference fp8_quant_bmm_test.py:227-237: fp8 output saturates at +-448
     a = (rand((1, 64, 128), 6).float() * 4).bfloat16()
