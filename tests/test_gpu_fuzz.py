@@ -120,6 +120,8 @@ def _fused_case(i):
         "b_k": bool(rng.integers(2)),
         "wq": bool(rng.integers(2)),
         "always": bool(rng.integers(2)),
+        # drawn last, so the draws above (and the cases they give) are unchanged
+        "epi": str(rng.choice(["none", "none", "bias_gelu", "bias_f32", "out_f32_gelu"])),
     }
 
 
@@ -129,7 +131,10 @@ def test_random_fused_quant_bmm_case(dev, i):
     the streaming kernel's envelope (N <= 256, K % 256 == 0, quant-N blocks
     >= 128): the quantized A is the 1 x 128 quantizer's bit for bit, the
     product equals quantize-then-multiply to fp32 rounding and is within
-    max-abs-rel 1e-2 of the fp64 product of the dequantized operands."""
+    max-abs-rel 1e-2 of the fp64 product of the dequantized operands. The
+    epilogue draw adds a bf16 bias with GELU, an fp32 bias, or GELU into an
+    fp32 output; a 16-bit output with an epilogue is held to one unit in the
+    last place of quantize-then-multiply."""
     from practice_cuda_amd.impls.hip_per_block import hip_per_block_bmm, hip_per_block_bmm_quant_a
     c = _fused_case(i)
     print(f"fused quant bmm fuzz {i}: {c}", flush=True)
@@ -139,15 +144,24 @@ def test_random_fused_quant_bmm_case(dev, i):
     if c["b_k"]:
         w = w.transpose(-1, -2).contiguous().transpose(-1, -2)
     qb = hip_per_block_quant(w.bfloat16().to(dev), block_m=128, block_n=c["qbn"], fp8_dtype=FMT[c["fmt"]])
-    res = hip_per_block_bmm_quant_a(x, qb, return_quant=c["wq"], always_fused=c["always"])
+    bias = None
+    if c["epi"] in ("bias_gelu", "bias_f32"):
+        bias = torch.randn(c["b"], c["m"], c["n"], generator=g).to(
+            torch.bfloat16 if c["epi"] == "bias_gelu" else torch.float32).to(dev)
+    epi = {"bias": bias, "activation": "gelu" if c["epi"] in ("bias_gelu", "out_f32_gelu") else "none",
+           "out_dtype": torch.float32 if c["epi"] == "out_f32_gelu" else torch.bfloat16}
+    res = hip_per_block_bmm_quant_a(x, qb, return_quant=c["wq"], always_fused=c["always"], **epi)
     out, qa = res if c["wq"] else (res, None)
     ref_q = hip_per_block_quant(x, block_m=1, block_n=128, fp8_dtype=FMT[c["fmt"]])
-    unfused = hip_per_block_bmm(ref_q, qb)
+    unfused = hip_per_block_bmm(ref_q, qb, **epi)
     torch.cuda.synchronize()
     if qa is not None:
         assert torch.equal(qa.tensor.view(torch.uint8), ref_q.tensor.view(torch.uint8))
         assert torch.equal(qa.dequant_scale.view(torch.int32), ref_q.dequant_scale.view(torch.int32))
+    assert out.dtype == epi["out_dtype"]
     scale = unfused.float().abs().max().item()
-    assert (out.float() - unfused.float()).abs().max().item() <= 1e-6 * scale + 1e-30
-    ref = O.bmm_reference(ref_q.dequantize().double().cpu().numpy(), qb.dequantize().double().cpu().numpy())
+    tol = 8e-3 if c["epi"] in ("bias_gelu", "bias_f32") else 1e-6
+    assert (out.float() - unfused.float()).abs().max().item() <= tol * scale + 1e-30
+    ref = O.bmm_reference(ref_q.dequantize().double().cpu().numpy(), qb.dequantize().double().cpu().numpy(),
+                          None if bias is None else bias.double().cpu().numpy(), epi["activation"])
     assert O.max_abs_rel(out.float().cpu().numpy(), ref) <= 1e-2
