@@ -75,6 +75,9 @@ def parse():
     p.add_argument("--pmc-probe-bmm", action="store_true",
                    help="eager launches for rocprofv3 --pmc passes: 3 plain bf16 copies of 256 MiB, then 3 "
                         "each of config 4 and the config-5 forward, dgrad, wgrad and layer wgrad")
+    p.add_argument("--pmc-probe-fused", action="store_true",
+                   help="eager launches for rocprofv3 --pmc passes: 3 plain bf16 copies of 256 MiB, then 3 "
+                        "fused quant-A BMMs each at N = 128 and N = 256 (M = 32768, K = 4096)")
     p.add_argument("--pmc-probe", action="store_true",
                    help="eager launches for rocprofv3 --pmc passes: 3 plain bf16 copies of "
                         "256 MiB (calibration) then 3 config-2 quantizations")
@@ -829,6 +832,33 @@ def pmc_probe_bmm(torch, dev):
                       "order": ["copy x3", "config4 x3"] + [f"{k} x3" for k in gemms]}))
 
 
+def pmc_probe_fused(torch, dev):
+    """Eager launches for rocprofv3 --pmc passes over the streaming fused
+    quant-A BMM, each dispatch carrying its own counters: three 256 MiB bf16
+    copies (calibration), then three launches each at N = 128 and N = 256 of
+    bf16 A [32768, 4096] (two tensors in turn) times e4m3fn B [4096, N],
+    128x128 B scales, bf16 C - the shapes of `--fused`."""
+    from practice_cuda_amd.impls.hip_per_block import hip_per_block_bmm_quant_a, hip_per_block_quant
+    src = torch.ones(1 << 27, dtype=torch.bfloat16, device=dev)  # 256 MiB
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    del src, dst
+    g = torch.Generator(device=dev).manual_seed(0)
+    m, k = 32768, 4096
+    xs = [torch.randn(1, m, k, generator=g, device=dev).bfloat16() for _ in range(2)]
+    for n in (128, 256):
+        qb = hip_per_block_quant((torch.randn(1, k, n, generator=g, device=dev) * 0.02).bfloat16(),
+                                 block_m=128, block_n=128)
+        out = torch.empty(1, m, n, device=dev, dtype=torch.bfloat16)
+        for i in range(3):
+            hip_per_block_bmm_quant_a(xs[i % 2], qb, out=out)
+        torch.cuda.synchronize()
+    print(json.dumps({"copy_bytes_read": (1 << 28), "copy_bytes_written": (1 << 28),
+                      "order": ["copy x3", "fused n=128 x3", "fused n=256 x3"]}))
+
+
 def mem_ceiling(torch, dev, steps, warmup):
     """What plain memory-bound kernels (PyTorch's own elementwise kernels)
     reach for the read:write mixes of this build's workloads, graph-timed
@@ -1116,6 +1146,9 @@ def main():
         return
     if args.pmc_probe_bmm:
         pmc_probe_bmm(torch, dev)
+        return
+    if args.pmc_probe_fused:
+        pmc_probe_fused(torch, dev)
         return
     if args.mem_ceiling:
         mem_ceiling(torch, dev, args.steps, args.warmup)
