@@ -145,6 +145,27 @@ def test_fused_bias_layouts(dev, bias_layout):
     assert (out.float() - ref.float()).abs().max().item() <= 8e-3 * ref.float().abs().max().item()
 
 
+@pytest.mark.parametrize("act", ["none", "gelu"])
+def test_fused_out_rows_not_8_byte_aligned(dev, act):
+    """An `out` whose row pitch (N + 2 elements) leaves rows off 8-byte
+    alignment takes the per-element epilogue; the columns past N are never
+    written."""
+    print(f"fused unaligned out rows {act}", flush=True)
+    n, k = 128, 512
+    x = _rand((2, 200, k), 31).to(dev)
+    qb = _b_operand(2, k, n, 32, dev)
+    bias = _rand((2, 200, n), 33).to(dev) if act == "gelu" else None
+    buf = torch.full((2, 200, n + 2), 7.0, device=dev, dtype=torch.bfloat16)
+    out = buf[..., :n]
+    r = hip_per_block_bmm_quant_a(x, qb, out=out, bias=bias, activation=act, always_fused=True)
+    qa = hip_per_block_quant(x, block_m=1, block_n=128)
+    ref = hip_per_block_bmm(qa, qb, bias=bias, activation=act)
+    torch.cuda.synchronize()
+    assert r.data_ptr() == out.data_ptr()
+    assert (out.float() - ref.float()).abs().max().item() <= 8e-3 * ref.float().abs().max().item()
+    assert torch.all(buf[..., n:] == 7.0)
+
+
 @pytest.mark.parametrize("layout", ["m_major", "unaligned_k"])
 def test_fused_falls_back_outside_envelope(dev, layout):
     """An M-major activation, or K not a multiple of 128, takes the quantizer +
