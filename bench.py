@@ -868,12 +868,19 @@ def mem_ceiling(torch, dev, steps, warmup):
     - 0:1 (config 4's output, 268 MB of its 311 MB): bf16 fill of [128, 2048, 512];
     and the 1:1 mix once more with this library's own streaming copy
     (pcamd_selftest_copy16: one 16-byte non-temporal load and store per lane)
-    at the shapes of config 5's dY and X."""
+    at the shapes of config 5's dY and X, and the 2:1 mix with its own
+    narrowing (pcamd_selftest_narrow16: the high byte of each bf16, two
+    16-byte loads and then two 8-byte stores per lane, the 1x128
+    quantizer's streaming layout) at the shapes of configs 2 and 1."""
     from practice_cuda_amd import _lib as L
 
     def hip_copy(src, dst):
         L.check(L.lib().pcamd_selftest_copy16(L.ptr(src), L.ptr(dst), src.numel() * src.element_size(),
                                               L.stream_of(src)), "pcamd_selftest_copy16")
+
+    def hip_narrow(src, dst):
+        L.check(L.lib().pcamd_selftest_narrow16(L.ptr(src), L.ptr(dst), src.numel() * src.element_size(),
+                                                L.stream_of(src)), "pcamd_selftest_narrow16")
 
     res = {}
     cases = {
@@ -882,9 +889,11 @@ def mem_ceiling(torch, dev, steps, warmup):
         "fill_bf16_128x2048x512": ((128, 2048, 512), lambda src, dst: dst.zero_(), torch.bfloat16, 2),
         "hip_copy_bf16_8192x14336": ((8192, 14336), hip_copy, torch.bfloat16, 4),
         "hip_copy_bf16_8192x4096": ((8192, 4096), hip_copy, torch.bfloat16, 4),
+        "hip_narrow_bf16_18432x7168": ((18432, 7168), hip_narrow, torch.uint8, 3),
+        "hip_narrow_bf16_4096x7168": ((4096, 7168), hip_narrow, torch.uint8, 3),
     }
     for name, (shape, op, odt, bpe) in cases.items():
-        nsets = 4
+        nsets = 8 if name == "hip_narrow_bf16_4096x7168" else 4  # config 1 is timed over 8 sets too
         srcs = [torch.randn(*shape, device=dev).bfloat16() for _ in range(nsets)] if bpe != 2 else [None] * nsets
         dsts = [torch.empty(*shape, dtype=odt, device=dev) for _ in range(nsets)]
         ms, _ = graph_time(torch, lambda i: op(srcs[i % nsets], dsts[i % nsets]), steps, warmup, settle_ms=SETTLE_MS)

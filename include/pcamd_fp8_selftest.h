@@ -4,8 +4,8 @@
  *
  * Not part of the product interface (include/pcamd_fp8.h): the test suite
  * calls them to pin the hardware fp8 conversion the quantizers use, and
- * bench.py to measure the plain-copy ceiling the quantizers are compared
- * with. They have no counterpart in the reference (xuOAO/practice_cuda),
+ * bench.py to measure the plain-copy and narrowing ceilings the quantizers
+ * are compared with. They have no counterpart in the reference (xuOAO/practice_cuda),
  * whose fp8 casts are Triton's `.to(fp8)`
  * (fp8_training/fp8_bench/kernels/quant/per_block.py:47).
  */
@@ -36,6 +36,18 @@ int pcamd_selftest_fp8_convert(int fmt, uint32_t *result, void *stream);
  * negative status.
  */
 int pcamd_selftest_copy16(const void *x, void *y, int64_t bytes, void *stream);
+
+/*
+ * Plain device narrowing: y receives the high byte of every 16-bit element
+ * of x (in_bytes a multiple of 16; x 16-byte and y 8-byte aligned; y holds
+ * in_bytes / 2 bytes), in the 1 x 128 quantizer's streaming layout: each
+ * lane loads two 16-byte chunks 64 apart (non-temporal) and then stores
+ * their 8-byte results (non-temporal), 256-thread workgroups. The
+ * quantizers' 2 : 1 read/write mix with no arithmetic, the ceiling they are
+ * measured against.
+ * Returns 0 or a negative status.
+ */
+int pcamd_selftest_narrow16(const void *x, void *y, int64_t in_bytes, void *stream);
 
 #ifdef __cplusplus
 }

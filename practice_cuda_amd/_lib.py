@@ -49,7 +49,7 @@ EXPORTED_SYMBOLS = (
     "pcamd_repack_fp8",
 )
 # test-only entry points (include/pcamd_fp8_selftest.h), exported by the same library
-TEST_SYMBOLS = ("pcamd_selftest_fp8_convert", "pcamd_selftest_copy16")
+TEST_SYMBOLS = ("pcamd_selftest_fp8_convert", "pcamd_selftest_copy16", "pcamd_selftest_narrow16")
 
 _i64 = ctypes.c_int64
 _int = ctypes.c_int
@@ -104,6 +104,8 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.pcamd_selftest_fp8_convert.argtypes = [_int, _ptr, _ptr]
     lib.pcamd_selftest_copy16.restype = _int
     lib.pcamd_selftest_copy16.argtypes = [_ptr, _ptr, _i64, _ptr]
+    lib.pcamd_selftest_narrow16.restype = _int
+    lib.pcamd_selftest_narrow16.argtypes = [_ptr, _ptr, _i64, _ptr]
 
 
 def lib() -> ctypes.CDLL:

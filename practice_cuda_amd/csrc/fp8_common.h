@@ -59,6 +59,7 @@ struct Chunk {
 };
 
 typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2_t __attribute__((ext_vector_type(2)));
 
 // 4 x 4 byte transpose: byte j of d[i] -> byte i of e[j]
 PCAMD_DEV void byte_transpose4(uint32_t d0, uint32_t d1, uint32_t d2, uint32_t d3, uint32_t (&e)[4]) {

@@ -1741,6 +1741,41 @@ extern "C" int pcamd_selftest_copy16(const void* x, void* y, int64_t bytes, void
   return check_launch("copy16_kernel");
 }
 
+// plain 2 : 1 streaming narrowing, y = the high byte of every 16-bit
+// element of x (measurement of the quantizers' read : write ceiling), in the
+// flat 1 x G quantizer's streaming layout: a wave owns 128 consecutive
+// 16-byte chunks, each lane loads chunks lane and lane + 64 (non-temporal)
+// before it stores their 8-byte results (non-temporal); 256-thread
+// workgroups
+__global__ __launch_bounds__(kGroupThreads) void narrow16_kernel(const u32x4_t* __restrict__ x,
+                                                              u32x2_t* __restrict__ y, int64_t chunks) {
+  const int64_t ch0 = (int64_t(blockIdx.x) * (kGroupThreads / 64) + (threadIdx.x >> 6)) * 128 + (threadIdx.x & 63);
+  u32x4_t v[2];
+#pragma unroll
+  for (int c = 0; c < 2; ++c) v[c] = ch0 + 64 * c < chunks ? __builtin_nontemporal_load(x + ch0 + 64 * c) : u32x4_t{};
+#pragma unroll
+  for (int c = 0; c < 2; ++c) {
+    // v_perm_b32: bytes 1 and 3 of the second operand, then of the first
+    const u32x2_t o = {__builtin_amdgcn_perm(v[c][1], v[c][0], 0x07050301u),
+                       __builtin_amdgcn_perm(v[c][3], v[c][2], 0x07050301u)};
+    if (ch0 + 64 * c < chunks) __builtin_nontemporal_store(o, y + ch0 + 64 * c);
+  }
+}
+
+extern "C" int pcamd_selftest_narrow16(const void* x, void* y, int64_t in_bytes, void* stream) {
+  clear_error();
+  if (in_bytes < 0 || in_bytes % 16) return set_error(PCAMD_ERR_INVALID, "in_bytes must be a non-negative multiple of 16");
+  if (in_bytes == 0) return PCAMD_OK;
+  if (!x || !y) return set_error(PCAMD_ERR_INVALID, "null pointer");
+  if ((reinterpret_cast<uintptr_t>(x) & 15) || (reinterpret_cast<uintptr_t>(y) & 7))
+    return set_error(PCAMD_ERR_INVALID, "x must be 16-byte and y 8-byte aligned");
+  const int64_t chunks = in_bytes / 16, grid = (chunks + 2 * kGroupThreads - 1) / (2 * kGroupThreads);
+  if (grid > INT32_MAX) return set_error(PCAMD_ERR_UNSUPPORTED, "narrowing too large");
+  narrow16_kernel<<<static_cast<uint32_t>(grid), kGroupThreads, 0, static_cast<hipStream_t>(stream)>>>(
+      static_cast<const u32x4_t*>(x), static_cast<u32x2_t*>(y), chunks);
+  return check_launch("narrow16_kernel");
+}
+
 extern "C" int pcamd_selftest_fp8_convert(int fmt, uint32_t* result, void* stream) {
   clear_error();
   if (!result) return set_error(PCAMD_ERR_INVALID, "null result pointer");

@@ -45,6 +45,13 @@ def test_test_only_symbols_live_in_their_own_header():
     assert L.pcamd_selftest_copy16(ctypes.c_void_p(0x10008), FAKE, 32, None) == -1
     assert b"aligned" in L.pcamd_last_error()
     assert L.pcamd_selftest_copy16(FAKE, FAKE, 0, None) == 0
+    assert L.pcamd_selftest_narrow16(FAKE, FAKE, 24, None) == -1
+    assert b"multiple of 16" in L.pcamd_last_error()
+    assert L.pcamd_selftest_narrow16(FAKE, ctypes.c_void_p(0x10004), 32, None) == -1
+    assert b"aligned" in L.pcamd_last_error()
+    assert L.pcamd_selftest_narrow16(None, FAKE, 32, None) == -1
+    assert b"null" in L.pcamd_last_error()
+    assert L.pcamd_selftest_narrow16(FAKE, FAKE, 0, None) == 0
 
 
 def test_abi_version_matches_header():

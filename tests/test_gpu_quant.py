@@ -73,6 +73,18 @@ def test_copy16_selftest(dev, nbytes):
     assert torch.equal(x, y)
 
 
+@pytest.mark.parametrize("nbytes", [16, 4096 * 16 + 48, 4096 * 7168 * 2])
+def test_narrow16_selftest(dev, nbytes):
+    # the 2:1 narrowing that bench.py --mem-ceiling times as the quantizers'
+    # ceiling: y is the high byte of every 16-bit element of x
+    x = torch.randint(0, 256, (nbytes,), dtype=torch.uint8, device=dev)
+    y = torch.zeros(nbytes // 2 + 8, dtype=torch.uint8, device=dev)
+    _lib.check(_lib.lib().pcamd_selftest_narrow16(_lib.ptr(x), _lib.ptr(y), nbytes, _lib.stream_of(x)), "narrow16")
+    torch.cuda.synchronize()
+    assert torch.equal(y[:nbytes // 2], x[1::2])
+    assert not y[nbytes // 2:].any()  # nothing written past in_bytes / 2
+
+
 @pytest.mark.parametrize("fmt", [_lib.E4M3FN, _lib.E5M2])
 def test_hw_convert_selftest(dev, fmt):
     res = torch.zeros(4, dtype=torch.int32, device=dev)
