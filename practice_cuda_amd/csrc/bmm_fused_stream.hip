@@ -78,8 +78,8 @@ struct ASlot {
 // finite, as in the quantizers)
 template <int DT, int FMT, bool B_K, int JN, int G, bool WQ, bool CLAMP>
 __global__ __launch_bounds__(NT, 1) void bmm_fused_stream_kernel(FastArgs a) {
-  static_assert(JN == 8 || JN == 16, "N up to 128 or 256");
-  static_assert(G == 1 || (G == 2 && JN == 8), "two K blocks per step: N up to 128");
+  static_assert(JN == 4 || JN == 8 || JN == 12 || JN == 16, "N up to 64, 128, 192 or 256");
+  static_assert(G == 1 || (G == 2 && JN <= 12), "two K blocks per step: N up to 192");
   constexpr int BCOLS = 16 * JN;                   // B columns per stage (K-major B: its rows)
   constexpr int B_BYTES = B_K ? BCOLS * BK : 256 * BK;  // one K block of B in LDS
   constexpr int SB_LOADS = JN > 8 ? 2 : 1;        // B block scales per K block (qbn >= 128)
@@ -356,7 +356,7 @@ int launch_wq(const FastArgs& a, int64_t batch, hipStream_t st) {
   if (clamp)
     return a.qa_out ? launch<DT, FMT, B_K, JN, 1, true, true>(a, batch, st)
                     : launch<DT, FMT, B_K, JN, 1, false, true>(a, batch, st);
-  if constexpr (JN == 8) {
+  if constexpr (JN <= 12) {
     if (a.k % (4 * BK) == 0 && !step_pairs_disabled())
       return a.qa_out ? launch<DT, FMT, B_K, JN, 2, true, false>(a, batch, st)
                       : launch<DT, FMT, B_K, JN, 2, false, false>(a, batch, st);
@@ -367,7 +367,10 @@ int launch_wq(const FastArgs& a, int64_t batch, hipStream_t st) {
 
 template <int DT, int FMT>
 int launch_dt(const FastArgs& a, bool b_k, int64_t batch, hipStream_t st) {
+  // 16-column sub-tiles per wave: the fewest of 4, 8, 12, 16 that cover N
+  if (a.n <= 64) return b_k ? launch_wq<DT, FMT, true, 4>(a, batch, st) : launch_wq<DT, FMT, false, 4>(a, batch, st);
   if (a.n <= 128) return b_k ? launch_wq<DT, FMT, true, 8>(a, batch, st) : launch_wq<DT, FMT, false, 8>(a, batch, st);
+  if (a.n <= 192) return b_k ? launch_wq<DT, FMT, true, 12>(a, batch, st) : launch_wq<DT, FMT, false, 12>(a, batch, st);
   return b_k ? launch_wq<DT, FMT, true, 16>(a, batch, st) : launch_wq<DT, FMT, false, 16>(a, batch, st);
 }
 
