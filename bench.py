@@ -1097,8 +1097,9 @@ def fused_probe(torch, dev, steps, warmup):
                                                        hip_per_block_bmm_quant_a, hip_per_block_quant)
     g = torch.Generator(device=dev).manual_seed(0)
     rows = []
-    for idx, (m, k, n) in enumerate([(32768, 4096, 128), (32768, 4096, 256), (16384, 4096, 512),
-                                     (8192, 4096, 1024), (8192, 4096, 4096), (8192, 4096, 14336)]):
+    for idx, (m, k, n) in enumerate([(32768, 4096, 64), (32768, 4096, 128), (32768, 4096, 192), (32768, 4096, 256),
+                                     (16384, 4096, 512), (8192, 4096, 1024), (8192, 4096, 4096),
+                                     (8192, 4096, 14336)]):
         # two A inputs in turn (2 x 268 MB at M = 32768: beyond the 256 MB MALL)
         xs = [torch.randn(1, m, k, generator=g, device=dev).bfloat16() for _ in range(2)]
         qb = hip_per_block_quant((torch.randn(1, k, n, generator=g, device=dev) * 0.02).bfloat16(),
