@@ -1093,7 +1093,7 @@ def fused_probe(torch, dev, steps, warmup):
     always_fused (the fused call inside the streaming kernel's envelope: here
     up to FUSED_MAX_N columns, K = 4096). Inside that envelope both paths are
     timed again with a bf16 bias [M, N] and GELU in the epilogue."""
-    from practice_cuda_amd.impls.hip_per_block import (_fused_streams, hip_per_block_bmm,
+    from practice_cuda_amd.impls.hip_per_block import (fused_streams, hip_per_block_bmm,
                                                        hip_per_block_bmm_quant_a, hip_per_block_quant)
     g = torch.Generator(device=dev).manual_seed(0)
     rows = []
@@ -1113,7 +1113,7 @@ def fused_probe(torch, dev, steps, warmup):
             hip_per_block_bmm(hip_per_block_quant(xs[i % 2], block_m=1, block_n=128), qb, out=out)
 
         unfused_ms, _ = graph_time(torch, unfused, steps, warmup)
-        streams = _fused_streams(n, k, 128)
+        streams = fused_streams(n, k, 128)
         rows.append({"m": m, "k": k, "n": n, "fused_us": round(fused_ms * 1e3, 1),
                      "quantize_then_multiply_us": round(unfused_ms * 1e3, 1),
                      "fused_speedup": round(unfused_ms / fused_ms, 3),

@@ -218,7 +218,7 @@ def hip_per_block_bmm(
 FUSED_MAX_N = 256
 
 
-def _fused_streams(n: int, k: int, qbn: int) -> bool:
+def fused_streams(n: int, k: int, qbn: int) -> bool:
     """Whether pcamd_bmm_quant_a runs its streaming kernel for this product
     (one workgroup holds all N columns and reads A once): the envelope of
     bmm_fused_stream_ok, for any bias, activation and output type. Outside it
@@ -291,7 +291,7 @@ def hip_per_block_bmm_quant_a(
         sa = torch.empty((batch, m, -(-k // 128)), device=x3.device, dtype=torch.float32)
     L = _lib.lib()
     rc = _lib.ERR_UNSUPPORTED
-    fused = always_fused or _fused_streams(n, k, qbn)
+    fused = always_fused or fused_streams(n, k, qbn)
     if in_b in ("n-major", "k-major") and x3.stride(-1) == 1 and fused:
         with torch.cuda.device(x3.device):
             rc = L.pcamd_bmm_quant_a(

@@ -189,3 +189,19 @@ def test_bmm_quant_a_invalid_arguments(over, rc, msg):
 def test_bmm_quant_a_empty_is_ok():
     assert _bmm_quant_a(M=0) == 0 and _bmm_quant_a(N=0) == 0 and _bmm_quant_a(B=0) == 0
     assert _lib.lib().pcamd_last_error() == b""
+
+
+@pytest.mark.parametrize("n,k,qbn,inside", [
+    (16, 256, 128, True), (64, 512, 128, True), (192, 4096, 256, True), (256, 256, 128, True),
+    (272, 4096, 128, False),   # wider than one workgroup's columns
+    (120, 4096, 128, False),   # N not a multiple of 16
+    (128, 384, 128, False),    # K not a multiple of 256
+    (128, 128, 128, False),    # K below two blocks
+    (128, 4096, 64, False),    # quant-N blocks under 128
+    (0, 4096, 128, False),
+])
+def test_fused_streams_envelope(n, k, qbn, inside):
+    # the products hip_per_block_bmm_quant_a sends to the fused entry point by
+    # default: the streaming kernel's envelope (bmm_fused_stream_ok)
+    from practice_cuda_amd.impls.hip_per_block import fused_streams
+    assert fused_streams(n, k, qbn) is inside
