@@ -94,6 +94,12 @@ def test_bmm_replay(dev):
     b4 = torch.randn(2, 512, 256, generator=g).bfloat16().to(dev)  # N = 256
     qb3 = hip_per_block_quant(b3, block_m=128, block_n=128)
     qb4 = hip_per_block_quant(b4, block_m=128, block_n=128)
+    b5 = torch.randn(2, 512, 192, generator=g).bfloat16().to(dev)  # N = 192: 12 sub-tiles, two K blocks per step
+    b6 = torch.randn(2, 512, 64, generator=g).bfloat16().to(dev)   # N = 64: 4 sub-tiles
+    qb5 = hip_per_block_quant(b5, block_m=128, block_n=128)
+    qb6 = hip_per_block_quant(b6, block_m=128, block_n=128)
+    bias5 = torch.randn(2, 512, 192, generator=g).bfloat16().to(dev)
+    bias_w = torch.randn(2, 512, 384, generator=g).bfloat16().to(dev)
     fns = {
         "wide": lambda: hip_per_block_bmm(qa, qb),
         "single": lambda: hip_per_block_bmm(qa1, qb1),
@@ -101,5 +107,10 @@ def test_bmm_replay(dev):
         "fused_stream_n128": lambda: hip_per_block_bmm_quant_a(ah, qb3, return_quant=True),
         "fused_stream_n256": lambda: hip_per_block_bmm_quant_a(ah, qb4),
         "fused_tiled": lambda: hip_per_block_bmm_quant_a(ah, qb, always_fused=True),
+        # epilogues: 16-bit bias + GELU (8-byte loads and stores), fp32 output
+        # (per-element), and the wide GEMM's LDS-staged bias + GELU
+        "fused_stream_n192_bias_gelu": lambda: hip_per_block_bmm_quant_a(ah, qb5, bias=bias5, activation="gelu"),
+        "fused_stream_n64_f32": lambda: hip_per_block_bmm_quant_a(ah, qb6, out_dtype=torch.float32),
+        "wide_bias_gelu": lambda: hip_per_block_bmm(qa, qb, bias=bias_w, activation="gelu"),
     }
     _replay_matches_eager(dev, fns)
