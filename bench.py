@@ -1142,7 +1142,8 @@ def main():
     args = parse()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on exactly one GPU; --gpus must be 1 "
-                          "(multi-GPU sharding is documented in DESIGN.md, not launched)"}))
+                          "(the path shards by rows and batch with no exchange for the quantizers; "
+                          "multi-GPU runs are not launched)"}))
         sys.exit(2)
     import torch
 
