@@ -184,3 +184,30 @@ def test_scales_are_quant(dev, kernel, mode, out):
     else:
         _bmm_abi(ad, bd, c0, (1.0 / (qsa * qsb)).to(dev), qsb.to(dev), code, 0)
     assert O.max_abs_rel(c0.float().cpu().numpy(), ref) <= tol
+
+
+@pytest.mark.parametrize("n", [64, 192, 256])
+def test_fused_quant_bmm_bench_shape(dev, n):
+    """The fused activation-quant BMM at the shape bench.py --fused times
+    (bf16 A [32768, 4096], e4m3fn B [4096, N] with 128x128 scales), with the
+    quantized A written out: those bytes and scales are the 1x128 quantizer's
+    bit for bit, the product equals quantize-then-multiply to fp32 rounding,
+    and every 64x64 output tile is within the bar of an fp32 GEMM of the
+    dequantized operands."""
+    from practice_cuda_amd.impls.hip_per_block import hip_per_block_bmm_quant_a
+    g = torch.Generator().manual_seed(n)
+    x = torch.randn(1, 32768, 4096, generator=g).bfloat16().to(dev)
+    qb = hip_per_block_quant((torch.randn(1, 4096, n, generator=g) * 0.02).bfloat16().to(dev),
+                             block_m=128, block_n=128)
+    print(f"fused quant bmm full size n={n}", flush=True)
+    out, qa = hip_per_block_bmm_quant_a(x, qb, return_quant=True)
+    ref_q = hip_per_block_quant(x, block_m=1, block_n=128)
+    unfused = hip_per_block_bmm(ref_q, qb)
+    torch.cuda.synchronize()
+    assert torch.equal(qa.tensor.view(torch.uint8), ref_q.tensor.view(torch.uint8))
+    assert torch.equal(qa.dequant_scale.view(torch.int32), ref_q.dequant_scale.view(torch.int32))
+    scale = unfused.float().abs().max().item()
+    assert (out.float() - unfused.float()).abs().max().item() <= 1e-6 * scale
+    ref = torch.matmul(ref_q.dequantize()[0], qb.dequantize()[0].contiguous())
+    err = _tile_err(out[0], ref, tile=64)
+    assert err <= TOL, err
