@@ -146,11 +146,20 @@ __global__ __launch_bounds__(NT, 1) void bmm_fused_stream_kernel(FastArgs a) {
   // lanes (16 apart): pcamd_quant_block's math
   auto quantize = [&](const ASlot<G>& s, int c0, int kb, v8i& f) -> float {
     float amax = 0.0f;
+    if constexpr (DT == kBF16) {
+      // |x| of all 32 values as one unsigned 16-bit max over the raw pairs,
+      // then the larger half (non-negative bf16 order like their bits)
+      uint32_t m = bf16_abs2(static_cast<uint32_t>(s.c[c0][0]));
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      Chunk<DT> ch;
-      ch.r[0] = make_uint4(s.c[c0 + c][0], s.c[c0 + c][1], s.c[c0 + c][2], s.c[c0 + c][3]);
-      amax = fmaxf(amax, chunk_amax<DT>(ch));
+      for (int w = 1; w < 16; ++w) m = pk_max_u16(m, bf16_abs2(static_cast<uint32_t>(s.c[c0 + w / 4][w % 4])));
+      amax = bf16_bits(max_halves(m));
+    } else {
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        Chunk<DT> ch;
+        ch.r[0] = make_uint4(s.c[c0 + c][0], s.c[c0 + c][1], s.c[c0 + c][2], s.c[c0 + c][3]);
+        amax = fmaxf(amax, chunk_amax<DT>(ch));
+      }
     }
     // non-negative floats order like their bits
     uint32_t u = __float_as_uint(amax);
